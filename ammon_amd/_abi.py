@@ -1,0 +1,137 @@
+"""ctypes binding of ``include/ammon/ammon.h`` (the C ABI of libammon_amd.so).
+
+This is the Python-side counterpart of the FFI crate a Rust host would bind:
+plain pointers and sizes, status codes turned into exceptions.  It loads the
+in-tree ``ammon_amd/libammon_amd.so`` only; if the library is missing the
+import fails loudly -- there is no CPU fallback.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libammon_amd.so")
+
+OK, E_VALIDATION, E_HIP, E_OOM, E_NO_DEVICE = 0, 1, 2, 3, 4
+F32, BF16 = 0, 1
+COPY_H2D, COPY_D2H, COPY_D2D = 1, 2, 3
+STREAM_VALIDATE = ctypes.c_void_p(1)
+
+ATTENTION_SPLIT_REF = 8
+ATTENTION_MAX_HEAD = 128
+DEFAULT_ROPE_THETA = 10000.0
+
+_P = ctypes.c_void_p
+_U32 = ctypes.c_uint32
+_I32 = ctypes.c_int32
+_U64 = ctypes.c_uint64
+_F = ctypes.c_float
+_SZ = ctypes.c_size_t
+_ST = ctypes.c_int  # ammon_status
+_DT = ctypes.c_int  # ammon_dtype
+
+
+class DecodeStep(ctypes.Structure):
+    """ammon_decode_step: {token, position} (reference src/kernels.rs:10-15)."""
+    _fields_ = [("token", _U32), ("position", _U32)]
+
+
+class DeviceInfo(ctypes.Structure):
+    _fields_ = [("device", ctypes.c_int), ("compute_units", ctypes.c_int),
+                ("max_shared_per_block", ctypes.c_int), ("warp_size", ctypes.c_int),
+                ("total_memory", _SZ), ("arch", ctypes.c_char * 64),
+                ("name", ctypes.c_char * 128)]
+
+
+# name -> (restype, argtypes).  Keep in the order of include/ammon/ammon.h.
+SIGNATURES = {
+    "ammon_runtime_create": (_ST, [ctypes.c_int, ctypes.POINTER(_P)]),
+    "ammon_runtime_release": (_ST, [_P]),
+    "ammon_last_error": (ctypes.c_char_p, []),
+    "ammon_abi_version": (ctypes.c_int, []),
+    "ammon_runtime_info": (_ST, [_P, ctypes.POINTER(DeviceInfo)]),
+    "ammon_alloc": (_ST, [_P, _SZ, ctypes.POINTER(_P)]),
+    "ammon_free": (_ST, [_P, _P]),
+    "ammon_alloc_host": (_ST, [_P, _SZ, ctypes.POINTER(_P)]),
+    "ammon_free_host": (_ST, [_P, _P]),
+    "ammon_memcpy": (_ST, [_P, _P, _P, _SZ, ctypes.c_int, _P]),
+    "ammon_stream_create": (_ST, [_P, ctypes.POINTER(_P)]),
+    "ammon_stream_destroy": (_ST, [_P, _P]),
+    "ammon_stream_synchronize": (_ST, [_P, _P]),
+    "ammon_event_create": (_ST, [_P, ctypes.POINTER(_P)]),
+    "ammon_event_destroy": (_ST, [_P, _P]),
+    "ammon_event_record": (_ST, [_P, _P, _P]),
+    "ammon_event_synchronize": (_ST, [_P, _P]),
+    "ammon_event_elapsed_ms": (_ST, [_P, _P, _P, ctypes.POINTER(_F)]),
+    "ammon_fill": (_ST, [_P, _P, _P, _DT, _SZ, _F]),
+    "ammon_fill_normal": (_ST, [_P, _P, _P, _DT, _SZ, _U64, _U64, _F, _F]),
+    "ammon_rope_table_bytes": (_SZ, [_U32, _U32]),
+    "ammon_rope_table_host": (_ST, [_F, _U32, _U32, _P]),
+    "ammon_kv_unpermute": (_ST, [_P, _P, _U32, _U32, _U32, _U32]),
+    "ammon_kv_permute": (_ST, [_P, _P, _U32, _U32, _U32, _U32]),
+    "ammon_attention_splits": (_U32, [_U32, _U32]),
+    "ammon_attention_scratch_bytes": (_SZ, [_U32, _U32, _U32, _U32]),
+    "ammon_attention_default_split": (_U32, [_P, _U32, _U32]),
+    "ammon_embed": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _P]),
+    "ammon_embed_rows": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P]),
+    "ammon_rmsnorm": (_ST, [_P, _P, _P, _P, _DT, _P, _U32, _U32, _F]),
+    "ammon_rope_store": (_ST, [_P, _P, _P, _U32, _P, _U32, _U32, _P, _DT, _U32, _P, _P]),
+    "ammon_rope": (_ST, [_P, _P, _P, _U32, _U32, _U32, _P, _DT, _U32, _P, _P]),
+    "ammon_cache_store": (_ST, [_P, _P, _P, _U32, _U32, _P, _DT, _U32, _P]),
+    "ammon_attention_partial": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _U32, _P,
+                                      _U32, _P]),
+    "ammon_attention_combine": (_ST, [_P, _P, _P, _U32, _U32, _U32, _P, _U32, _P]),
+    "ammon_attention_decode": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _U32, _P,
+                                     _U32, _P, _SZ, _P]),
+    "ammon_swiglu": (_ST, [_P, _P, _P, _P, _U32]),
+    "ammon_add": (_ST, [_P, _P, _P, _P, _P, _U32]),
+    "ammon_gemv": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _P, _P]),
+    "ammon_gemv_rmsnorm": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _DT, _U32, _U32, _P]),
+    "ammon_qkv_rope_store": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _P, _DT, _U32, _U32, _U32,
+                                   _U32, _P, _P, _P, _DT, _U32, _P, _P]),
+    "ammon_gate_up_swiglu": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _DT, _U32, _U32, _P]),
+    "ammon_argmax_scratch_bytes": (_SZ, [_U32]),
+    "ammon_argmax": (_ST, [_P, _P, _P, _U32, _P, _P]),
+    "ammon_greedy_next": (_ST, [_P, _P, _P, _U32, _P, _P, _U32, _P, _P, _U32]),
+}
+
+
+class AmmonError(RuntimeError):
+    """A non-OK ammon_status with the library's thread-local message."""
+
+    def __init__(self, status: int, message: str):
+        super().__init__(f"[status {status}] {message}")
+        self.status = status
+        self.message = message
+
+
+def _load() -> ctypes.CDLL:
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is missing: build it with `python -c 'import __graft_entry__ as g; "
+            f"g.build()'` (make -C ammon_amd/csrc)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+lib = _load()
+
+
+def last_error() -> str:
+    msg = lib.ammon_last_error()
+    return msg.decode() if msg else ""
+
+
+def check(status: int) -> None:
+    if status != OK:
+        raise AmmonError(int(status), last_error())
+
+
+def call(name: str, *args) -> None:
+    """Call a status-returning ABI function and raise on failure."""
+    check(getattr(lib, name)(*args))

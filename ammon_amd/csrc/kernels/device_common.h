@@ -1,0 +1,154 @@
+// device_common.h -- shared gfx950 device helpers: bf16 conversion, 16-byte
+// chunk loads, wave64 and workgroup reductions.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../kernel_params.h"
+
+#define AMMON_DEV __device__ __forceinline__
+#define AMMON_WG 256
+#define AMMON_WAVES (AMMON_WG / 64)
+
+// ---- bf16 ------------------------------------------------------------------
+AMMON_DEV float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+AMMON_DEV float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+AMMON_DEV float bf16_to_f32(uint16_t h) { return __uint_as_float((uint32_t)h << 16); }
+
+// Round-to-nearest-even; NaN stays a (quiet) NaN.
+AMMON_DEV uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+AMMON_DEV void store_elem(void *base, uint32_t dtype, size_t i, float v) {
+  if (dtype == AMMON_K_BF16)
+    ((uint16_t *)base)[i] = f32_to_bf16(v);
+  else
+    ((float *)base)[i] = v;
+}
+
+AMMON_DEV float load_elem(const void *base, uint32_t dtype, size_t i) {
+  if (dtype == AMMON_K_BF16) return bf16_to_f32(((const uint16_t *)base)[i]);
+  return ((const float *)base)[i];
+}
+
+// ---- chunk loads -----------------------------------------------------------
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Chunk<T, CH>: CH consecutive elements of storage type T (float or bf16
+// stored as uint16_t) loaded with one vector load and widened to fp32.
+template <typename T, int CH> struct Chunk;
+
+template <> struct Chunk<uint16_t, 8> {
+  using V = u32x4;
+  static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
+  static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
+  static AMMON_DEV V zero() { return V{0u, 0u, 0u, 0u}; }
+  static AMMON_DEV void widen(V v, float *f) {
+    f[0] = bf16_lo(v[0]); f[1] = bf16_hi(v[0]);
+    f[2] = bf16_lo(v[1]); f[3] = bf16_hi(v[1]);
+    f[4] = bf16_lo(v[2]); f[5] = bf16_hi(v[2]);
+    f[6] = bf16_lo(v[3]); f[7] = bf16_hi(v[3]);
+  }
+};
+
+template <> struct Chunk<uint16_t, 4> {
+  using V = u32x2;
+  static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
+  static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
+  static AMMON_DEV V zero() { return V{0u, 0u}; }
+  static AMMON_DEV void widen(V v, float *f) {
+    f[0] = bf16_lo(v[0]); f[1] = bf16_hi(v[0]);
+    f[2] = bf16_lo(v[1]); f[3] = bf16_hi(v[1]);
+  }
+};
+
+template <> struct Chunk<uint16_t, 2> {
+  using V = uint32_t;
+  static AMMON_DEV V load(const uint16_t *p) { return *(const uint32_t *)p; }
+  static AMMON_DEV V load_nt(const uint16_t *p) {
+    return __builtin_nontemporal_load((const uint32_t *)p);
+  }
+  static AMMON_DEV V zero() { return 0u; }
+  static AMMON_DEV void widen(V v, float *f) { f[0] = bf16_lo(v); f[1] = bf16_hi(v); }
+};
+
+template <> struct Chunk<uint16_t, 1> {
+  using V = uint16_t;
+  static AMMON_DEV V load(const uint16_t *p) { return *p; }
+  static AMMON_DEV V load_nt(const uint16_t *p) { return *p; }
+  static AMMON_DEV V zero() { return 0; }
+  static AMMON_DEV void widen(V v, float *f) { f[0] = bf16_to_f32(v); }
+};
+
+template <> struct Chunk<float, 4> {
+  using V = f32x4;
+  static AMMON_DEV V load(const float *p) { return *(const V *)p; }
+  static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
+  static AMMON_DEV V zero() { return V{0.f, 0.f, 0.f, 0.f}; }
+  static AMMON_DEV void widen(V v, float *f) { f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3]; }
+};
+
+template <> struct Chunk<float, 2> {
+  using V = f32x2;
+  static AMMON_DEV V load(const float *p) { return *(const V *)p; }
+  static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
+  static AMMON_DEV V zero() { return V{0.f, 0.f}; }
+  static AMMON_DEV void widen(V v, float *f) { f[0] = v[0]; f[1] = v[1]; }
+};
+
+template <> struct Chunk<float, 1> {
+  using V = float;
+  static AMMON_DEV V load(const float *p) { return *p; }
+  static AMMON_DEV V load_nt(const float *p) { return *p; }
+  static AMMON_DEV V zero() { return 0.f; }
+  static AMMON_DEV void widen(V v, float *f) { f[0] = v; }
+};
+
+// ---- reductions --------------------------------------------------------------
+// Butterfly reductions: every participating lane ends with the identical
+// value, and the association order is fixed, so results are deterministic.
+template <int WIDTH = 64> AMMON_DEV float wave_sum(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <int WIDTH = 64> AMMON_DEV float wave_max(float v) {
+#pragma unroll
+  for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+// Sum over a 256-thread workgroup; `red` must hold AMMON_WAVES floats.  The
+// wave totals are added in wave order.  Contains barriers: call uniformly.
+AMMON_DEV float block_sum(float v, float *red) {
+  v = wave_sum(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < AMMON_WAVES; ++w) t += red[w];
+  __syncthreads();
+  return t;
+}
+
+AMMON_DEV float block_max(float v, float *red) {
+  v = wave_max(v);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (lane == 0) red[wave] = v;
+  __syncthreads();
+  float t = red[0];
+#pragma unroll
+  for (int w = 1; w < AMMON_WAVES; ++w) t = fmaxf(t, red[w]);
+  __syncthreads();
+  return t;
+}

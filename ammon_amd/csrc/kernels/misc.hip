@@ -1,0 +1,137 @@
+// misc.hip -- elementwise SwiGLU and residual add, the greedy argmax with
+// DecodeStep feedback, and fills for synthetic weights and scratch clearing.
+#include "device_common.h"
+
+// hb = silu(hb) * hb2 in the reference's order (src/kernels.rs:462-476).
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_swiglu(ammon_k_elementwise p) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.n) return;
+  float val = p.hb[i];
+  val = val * (1.0f / (1.0f + expf(-val)));
+  val = val * p.b[i];
+  p.hb[i] = val;
+}
+
+// out = a + b (Goldy add_into as used for residuals, src/blocks.rs:256-257).
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_add(ammon_k_elementwise p) {
+  const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= p.n) return;
+  p.hb[i] = p.a[i] + p.b[i];
+}
+
+// ---- argmax ------------------------------------------------------------------
+// sample_argmax (reference src/tokenizer.rs:179-189) returns the first index
+// of the maximum under a strict `>` scan from logits[0]: NaN never wins, and a
+// NaN logits[0] yields 0.  In parallel: every non-NaN element is a candidate,
+// candidates combine by (larger value, then lower index) -- a total order, so
+// the tree shape cannot change the answer -- and the NaN-logits[0] case is
+// applied at the end.  +0 and -0 compare equal, as in the scan.
+#define ARGMAX_NONE 0xffffffffu
+
+AMMON_DEV void cand_merge(float &v, uint32_t &i, float v2, uint32_t i2) {
+  if (i2 == ARGMAX_NONE) return;
+  if (i == ARGMAX_NONE || v2 > v || (!(v > v2) && i2 < i)) {
+    v = v2;
+    i = i2;
+  }
+}
+
+AMMON_DEV void block_cand_reduce(float &v, uint32_t &i) {
+  __shared__ float sv[AMMON_WG];
+  __shared__ uint32_t si[AMMON_WG];
+  sv[threadIdx.x] = v;
+  si[threadIdx.x] = i;
+  __syncthreads();
+  for (uint32_t s = AMMON_WG / 2; s > 0; s >>= 1) {
+    if (threadIdx.x < s) {
+      float a = sv[threadIdx.x];
+      uint32_t ai = si[threadIdx.x];
+      cand_merge(a, ai, sv[threadIdx.x + s], si[threadIdx.x + s]);
+      sv[threadIdx.x] = a;
+      si[threadIdx.x] = ai;
+    }
+    __syncthreads();
+  }
+  v = sv[0];
+  i = si[0];
+}
+
+// Pass 1: one candidate per workgroup.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_partial(ammon_k_argmax p) {
+  float v = 0.f;
+  uint32_t idx = ARGMAX_NONE;
+  for (uint32_t i = blockIdx.x * AMMON_WG + threadIdx.x; i < p.n; i += gridDim.x * AMMON_WG) {
+    const float x = p.logits[i];
+    if (x == x) cand_merge(v, idx, x, i);
+  }
+  block_cand_reduce(v, idx);
+  if (threadIdx.x == 0) {
+    p.cand_v[blockIdx.x] = v;
+    p.cand_i[blockIdx.x] = idx;
+  }
+}
+
+// Pass 2 (one workgroup): fold the candidates, apply the logits[0] rule, and
+// optionally feed the choice back into the device DecodeStep with the greedy
+// loop's prompt forcing (reference src/generate.rs:60-72):
+//   next = pos + 1 < n_prompt ? prompt[pos + 1] : argmax;  tokens[pos] = next;
+//   step = {next, pos + 1}.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_final(ammon_k_argmax p) {
+  float v = 0.f;
+  uint32_t idx = ARGMAX_NONE;
+  for (uint32_t b = threadIdx.x; b < p.blocks; b += AMMON_WG) cand_merge(v, idx, p.cand_v[b], p.cand_i[b]);
+  block_cand_reduce(v, idx);
+  if (threadIdx.x != 0) return;
+  const float first = p.logits[0];
+  int32_t best = (first != first || idx == ARGMAX_NONE) ? 0 : (int32_t)idx;
+  if (p.out) *p.out = best;
+  if (p.step) {
+    const uint32_t pos = p.step->position;
+    const int32_t next = (pos + 1 < p.n_prompt) ? p.prompt[pos + 1] : best;
+    if (p.tokens && pos < p.max_tokens) p.tokens[pos] = next;
+    p.step->token = (uint32_t)next;
+    p.step->position = pos + 1;
+  }
+}
+
+// ---- fills -----------------------------------------------------------------
+AMMON_DEV uint64_t splitmix64(uint64_t x) {
+  x += 0x9E3779B97F4A7C15ull;
+  x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
+  x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
+  return x ^ (x >> 31);
+}
+
+// Counter-based N(mean, std): element 2c and 2c+1 are the Box-Muller pair of
+// splitmix64(key ^ c * K).  Used for synthetic weights and KV contents.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_fill_normal(ammon_k_fill p) {
+#pragma clang fp contract(off)
+  const uint64_t key = splitmix64(p.seed ^ splitmix64(p.stream + 0x632BE59BD9B4E019ull));
+  const double two_pi = 6.283185307179586476925286766559;
+  const uint64_t pairs = (p.count + 1) / 2;
+  for (uint64_t c = (uint64_t)blockIdx.x * AMMON_WG + threadIdx.x; c < pairs;
+       c += (uint64_t)gridDim.x * AMMON_WG) {
+    const uint64_t bits = splitmix64(key ^ (c * 0xD1B54A32D192ED03ull));
+    const double u1 = ((double)(bits >> 32) + 0.5) * (1.0 / 4294967296.0);
+    const double u2 = ((double)(bits & 0xffffffffull) + 0.5) * (1.0 / 4294967296.0);
+    const double r = sqrt(-2.0 * log(u1));
+    double sn, cn;
+    sincos(two_pi * u2, &sn, &cn);
+    const float z0 = (float)((double)p.mean + (double)p.std * (r * cn));
+    const float z1 = (float)((double)p.mean + (double)p.std * (r * sn));
+    store_elem(p.dst, p.dtype, 2 * c, z0);
+    if (2 * c + 1 < p.count) store_elem(p.dst, p.dtype, 2 * c + 1, z1);
+  }
+}
+
+// Constant fill with a raw bit pattern (32-bit for f32, 16-bit for bf16).
+// Used instead of hipMemsetAsync so the launch can sit inside a graph.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_fill_const(ammon_k_fill p) {
+  for (uint64_t i = (uint64_t)blockIdx.x * AMMON_WG + threadIdx.x; i < p.count;
+       i += (uint64_t)gridDim.x * AMMON_WG) {
+    if (p.dtype == AMMON_K_BF16)
+      ((uint16_t *)p.dst)[i] = (uint16_t)p.bits;
+    else
+      ((uint32_t *)p.dst)[i] = p.bits;
+  }
+}

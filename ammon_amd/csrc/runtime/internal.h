@@ -1,0 +1,71 @@
+// internal.h -- shared state of the C-ABI implementation (host side only).
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstdarg>
+#include <cstdint>
+#include <string>
+#include <vector>
+
+#include "../kernel_params.h"
+#include "ammon/ammon.h"
+
+namespace ammon_rt {
+
+// Attention partial variants: [kv dtype][chunk index][G index].
+constexpr int kAttChunks = 4;  // CH = 8, 4, 2, 1
+constexpr int kAttGroups = 4;  // GMAX = 1, 2, 4, 8
+// GEMV variants: [weight dtype][vector?][mode].
+constexpr int kGemvModes = 4;
+
+struct Kernels {
+  hipFunction_t embed = nullptr;
+  hipFunction_t rmsnorm = nullptr;
+  hipFunction_t rope = nullptr;
+  hipFunction_t cache_store = nullptr;
+  hipFunction_t att_partial[2][kAttChunks][kAttGroups] = {};
+  hipFunction_t att_combine = nullptr;
+  hipFunction_t gemv[2][2][kGemvModes] = {};
+  hipFunction_t swiglu = nullptr;
+  hipFunction_t add = nullptr;
+  hipFunction_t argmax_partial = nullptr;
+  hipFunction_t argmax_final = nullptr;
+  hipFunction_t fill_normal = nullptr;
+  hipFunction_t fill_const = nullptr;
+};
+
+// LDS per compute unit on gfx950 (bytes); bounds resident GEMV workgroups.
+constexpr uint32_t kLdsPerCu = 160 * 1024;
+
+// GEMV rows per wave and waves per workgroup (must match gemv.hip).
+constexpr uint32_t kGemvRowsPerWave = 2;
+constexpr uint32_t kGemvWaves = 4;
+constexpr uint32_t kWorkgroup = 256;
+
+ammon_status set_error(ammon_status st, const char *fmt, ...)
+    __attribute__((format(printf, 2, 3)));
+ammon_status hip_error(hipError_t e, const char *what);
+
+}  // namespace ammon_rt
+
+struct ammon_runtime {
+  int device = 0;
+  int refs = 0;
+  hipStream_t stream = nullptr;
+  std::vector<hipModule_t> modules;
+  ammon_rt::Kernels k;
+  ammon_device_info info = {};
+  uint32_t gemv_wgs_per_cu = 4;
+};
+
+#define AMMON_HIP(expr)                                            \
+  do {                                                             \
+    hipError_t _e = (expr);                                        \
+    if (_e != hipSuccess) return ammon_rt::hip_error(_e, #expr);   \
+  } while (0)
+
+#define AMMON_CHECK(cond, ...)                                                \
+  do {                                                                        \
+    if (!(cond)) return ammon_rt::set_error(AMMON_E_VALIDATION, __VA_ARGS__); \
+  } while (0)

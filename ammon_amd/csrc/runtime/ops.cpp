@@ -1,0 +1,577 @@
+// ops.cpp -- C-ABI kernel entry points: validate, pick the variant, launch.
+//
+// Each entry point replaces one reference kernel record + dispatch (or one
+// fused group of them); the reference file:line is given in ammon.h.  All
+// validation happens before anything is enqueued, so a failed call leaves
+// the stream untouched -- the counterpart of a failed Goldy record leaving
+// the scheme's IR unchanged (reference tests/kernels.rs:125-146).
+#include <hip/hip_runtime_api.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+
+#include "internal.h"
+
+using namespace ammon_rt;
+
+namespace {
+
+struct DeviceGuard {
+  int prev = -1;
+  explicit DeviceGuard(int device) {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != device) {
+      prev = cur;
+      (void)hipSetDevice(device);
+    }
+  }
+  ~DeviceGuard() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+};
+
+inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
+
+inline bool valid_dtype(ammon_dtype d) { return d == AMMON_F32 || d == AMMON_BF16; }
+inline size_t dsize(ammon_dtype d) { return d == AMMON_BF16 ? 2 : 4; }
+
+inline bool overlaps(const void *a, size_t abytes, const void *b, size_t bbytes) {
+  const uintptr_t a0 = (uintptr_t)a, b0 = (uintptr_t)b;
+  return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+template <typename P>
+ammon_status launch(ammon_runtime *rt, ammon_stream s, hipFunction_t f, uint32_t gx, uint32_t gy,
+                    uint32_t shmem, P &params, const char *what) {
+  if (gx == 0 || gy == 0) return AMMON_OK;
+  DeviceGuard guard(rt->device);
+  hipStream_t st = s ? (hipStream_t)s : rt->stream;
+  void *args[] = {&params};
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, kWorkgroup, 1, 1, shmem, st, args, nullptr);
+  if (e != hipSuccess) return hip_error(e, what);
+  return AMMON_OK;
+}
+
+#define REQUIRE_RT()                                              \
+  do {                                                            \
+    if (!rt) return set_error(AMMON_E_VALIDATION, "runtime is NULL"); \
+  } while (0)
+
+#define VALIDATE_ONLY()                                  \
+  do {                                                   \
+    if (stream == AMMON_STREAM_VALIDATE) return AMMON_OK; \
+  } while (0)
+
+// ---- GEMV family --------------------------------------------------------------
+struct GemvArgs {
+  int mode;
+  const void *w0, *w1, *w2;
+  ammon_dtype w_dtype;
+  uint32_t d, n, rows;
+  const float *x;
+  const void *norm_w;
+  ammon_dtype norm_dtype;
+  float eps;
+  const float *residual;
+  float *y;
+  void *k_cache, *v_cache;
+  const ammon_decode_step *step;
+  const float *table;
+  uint32_t kv_dim, head, seq;
+  ammon_dtype kv_dtype;
+};
+
+ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemvArgs &a,
+                                   const char *what) {
+  AMMON_CHECK(valid_dtype(a.w_dtype), "%s: unknown weight dtype %d", what, (int)a.w_dtype);
+  AMMON_CHECK(a.w0 && a.x && a.y, "%s: NULL weight, x or y", what);
+  AMMON_CHECK(a.n > 0 && a.d > 0, "%s: empty matrix (d=%u, n=%u)", what, a.d, a.n);
+  AMMON_CHECK(!a.norm_w || valid_dtype(a.norm_dtype), "%s: unknown norm dtype", what);
+  AMMON_CHECK(!a.norm_w || (std::isfinite(a.eps) && a.eps >= 0.f), "%s: eps must be finite and >= 0", what);
+  const size_t shmem = (size_t)a.n * sizeof(float);
+  AMMON_CHECK(shmem <= (size_t)rt->info.max_shared_per_block,
+              "%s: reduction length n=%u needs %zu bytes of LDS; the device allows %d", what, a.n,
+              shmem, rt->info.max_shared_per_block);
+  // y must not overlap x: x is staged by every workgroup while others write y.
+  size_t ybytes = (size_t)a.d * 4;
+  AMMON_CHECK(!overlaps(a.x, (size_t)a.n * 4, a.y, ybytes), "%s: y overlaps x", what);
+  if (a.residual)
+    AMMON_CHECK(!overlaps(a.x, (size_t)a.n * 4, a.residual, ybytes), "%s: residual overlaps x", what);
+  if (stream == AMMON_STREAM_VALIDATE) return AMMON_OK;
+
+  const int dt = a.w_dtype == AMMON_BF16 ? 1 : 0;
+  const uint32_t ch = dt ? 8 : 4;
+  uintptr_t bits = (uintptr_t)a.w0 | (uintptr_t)a.w1 | (uintptr_t)a.w2;
+  const int vec = (a.n % ch == 0) && (bits & 15u) == 0;
+
+  ammon_k_gemv p = {};
+  p.w0 = a.w0;
+  p.w1 = a.w1;
+  p.w2 = a.w2;
+  p.x = a.x;
+  p.norm_w = a.norm_w;
+  p.residual = a.residual;
+  p.y = a.y;
+  p.k_cache = a.k_cache;
+  p.v_cache = a.v_cache;
+  p.step = (const ammon_k_step *)a.step;
+  p.table = a.table;
+  p.d = a.d;
+  p.n = a.n;
+  p.rows = a.rows;
+  const uint32_t rows_per_wg = kGemvRowsPerWave * kGemvWaves;
+  p.row_blocks = cdiv(a.rows, rows_per_wg);
+  p.norm_dtype = (uint32_t)a.norm_dtype;
+  p.eps = a.eps;
+  p.kv_dim = a.kv_dim;
+  p.head = a.head;
+  p.seq = a.seq;
+  p.kv_dtype = (uint32_t)a.kv_dtype;
+
+  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
+  const uint32_t lds_fit = std::max<uint32_t>(1, (uint32_t)(kLdsPerCu / (shmem + 64)));
+  const uint32_t per_cu = std::min(rt->gemv_wgs_per_cu, lds_fit);
+  const uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * per_cu);
+  return launch(rt, stream, rt->k.gemv[dt][vec][a.mode], grid, 1, (uint32_t)shmem, p, what);
+}
+
+// ---- attention ------------------------------------------------------------------
+int att_chunk_index(ammon_dtype kv, uint32_t head, const void *k, const void *v) {
+  // CH = 8 (bf16 only), 4, 2, 1 -> index 0..3; the widest that divides head
+  // and keeps the cache bases aligned to a chunk.
+  const uintptr_t bits = (uintptr_t)k | (uintptr_t)v;
+  const size_t es = dsize(kv);
+  const int chs[4] = {8, 4, 2, 1};
+  for (int i = (kv == AMMON_BF16 ? 0 : 1); i < 4; ++i) {
+    const uint32_t ch = (uint32_t)chs[i];
+    if (head % ch == 0 && (bits % (ch * es)) == 0 && head / ch <= 64) return i;
+  }
+  return -1;
+}
+
+int att_group_index(uint32_t g) {
+  if (g <= 1) return 0;
+  if (g <= 2) return 1;
+  if (g <= 4) return 2;
+  if (g <= 8) return 3;
+  return -1;
+}
+
+ammon_status attention_check(ammon_runtime *rt, const char *what, uint32_t q_heads,
+                             uint32_t kv_heads, uint32_t head, uint32_t seq, uint32_t split_len) {
+  (void)rt;
+  AMMON_CHECK(q_heads > 0 && kv_heads > 0 && head > 0 && seq > 0,
+              "%s: empty shape (q_heads=%u, kv_heads=%u, head=%u, seq=%u)", what, q_heads,
+              kv_heads, head, seq);
+  AMMON_CHECK(head <= AMMON_ATTENTION_MAX_HEAD, "%s: head size %u exceeds %u", what, head,
+              AMMON_ATTENTION_MAX_HEAD);
+  AMMON_CHECK(q_heads % kv_heads == 0, "%s: q_heads %u is not a multiple of kv_heads %u", what,
+              q_heads, kv_heads);
+  AMMON_CHECK(q_heads / kv_heads <= 8, "%s: %u query heads per kv head exceeds 8", what,
+              q_heads / kv_heads);
+  AMMON_CHECK(split_len >= 1 && split_len <= AMMON_ATTENTION_MAX_SPLIT,
+              "%s: split length %u outside [1, %u]", what, split_len, AMMON_ATTENTION_MAX_SPLIT);
+  AMMON_CHECK(ammon_attention_splits(seq, split_len) <= AMMON_ATTENTION_MAX_SPLITS,
+              "%s: %u splits exceed %u; use a longer split", what,
+              ammon_attention_splits(seq, split_len), AMMON_ATTENTION_MAX_SPLITS);
+  return AMMON_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+// ---- embed ---------------------------------------------------------------------
+static ammon_status embed_impl(ammon_runtime *rt, ammon_stream stream, const void *table,
+                               ammon_dtype dt, uint32_t vocab, uint32_t dim,
+                               const ammon_decode_step *step, const uint32_t *ids, uint32_t rows,
+                               float *x, const char *what) {
+  REQUIRE_RT();
+  AMMON_CHECK(valid_dtype(dt), "%s: unknown table dtype %d", what, (int)dt);
+  AMMON_CHECK(table && x, "%s: NULL table or x", what);
+  AMMON_CHECK(ids || step, "%s: no token source", what);
+  AMMON_CHECK(vocab > 0 && dim > 0, "%s: empty table (vocab=%u, dim=%u)", what, vocab, dim);
+  VALIDATE_ONLY();
+  ammon_k_embed p = {table, (const ammon_k_step *)step, ids, x, vocab, dim, rows, (uint32_t)dt};
+  const uint32_t per_lane = dt == AMMON_BF16 ? 8 : 4;
+  const uint32_t gx = std::min<uint32_t>(cdiv(dim, (uint64_t)kWorkgroup * per_lane), 64);
+  return launch(rt, stream, rt->k.embed, gx, rows, 0, p, what);
+}
+
+ammon_status ammon_embed(ammon_runtime *rt, ammon_stream stream, const void *table,
+                         ammon_dtype table_dtype, uint32_t vocab, uint32_t dim,
+                         const ammon_decode_step *step, float *x) {
+  AMMON_CHECK(step != nullptr, "embed: parameter `step` is NULL");
+  return embed_impl(rt, stream, table, table_dtype, vocab, dim, step, nullptr, 1, x, "embed");
+}
+
+ammon_status ammon_embed_rows(ammon_runtime *rt, ammon_stream stream, const void *table,
+                              ammon_dtype table_dtype, uint32_t vocab, uint32_t dim,
+                              const uint32_t *ids, uint32_t rows, float *x) {
+  AMMON_CHECK(ids != nullptr, "embed_rows: parameter `ids` is NULL");
+  AMMON_CHECK(rows <= 65535, "embed_rows: %u rows exceed 65535", rows);
+  return embed_impl(rt, stream, table, table_dtype, vocab, dim, nullptr, ids, rows, x,
+                    "embed_rows");
+}
+
+// ---- rmsnorm ----------------------------------------------------------------------
+ammon_status ammon_rmsnorm(ammon_runtime *rt, ammon_stream stream, const float *x,
+                           const void *weight, ammon_dtype weight_dtype, float *out,
+                           uint32_t rows, uint32_t dim, float eps) {
+  REQUIRE_RT();
+  AMMON_CHECK(x && weight && out, "rmsnorm: NULL x, weight or out");
+  AMMON_CHECK(valid_dtype(weight_dtype), "rmsnorm: unknown weight dtype %d", (int)weight_dtype);
+  AMMON_CHECK(dim > 0, "rmsnorm: `dim` is 0");
+  AMMON_CHECK(std::isfinite(eps) && eps >= 0.f, "rmsnorm: eps must be finite and >= 0");
+  AMMON_CHECK(out == x || !overlaps(x, (size_t)rows * dim * 4, out, (size_t)rows * dim * 4),
+              "rmsnorm: out partially overlaps x");
+  VALIDATE_ONLY();
+  ammon_k_rmsnorm p = {x, weight, out, rows, dim, (uint32_t)weight_dtype, eps};
+  return launch(rt, stream, rt->k.rmsnorm, rows, 1, 0, p, "rmsnorm");
+}
+
+// ---- rope / cache store ----------------------------------------------------------------
+static ammon_status rope_impl(ammon_runtime *rt, ammon_stream stream, float *q, uint32_t q_heads,
+                              const float *k_proj, uint32_t kv_heads, uint32_t head,
+                              void *k_cache, ammon_dtype kv_dtype, uint32_t seq,
+                              const ammon_decode_step *step, const float *table,
+                              const char *what) {
+  REQUIRE_RT();
+  AMMON_CHECK(q && k_cache && step && table, "%s: NULL q, k cache, step or table", what);
+  AMMON_CHECK(valid_dtype(kv_dtype), "%s: unknown kv dtype %d", what, (int)kv_dtype);
+  AMMON_CHECK(head >= 2 && head % 2 == 0, "%s: head size %u must be even", what, head);
+  AMMON_CHECK(q_heads > 0 && kv_heads > 0 && seq > 0, "%s: empty shape", what);
+  const uint64_t q_numel = (uint64_t)q_heads * head, kv_dim = (uint64_t)kv_heads * head;
+  AMMON_CHECK(kv_dim <= q_numel, "%s: kv width must be even and no wider than q", what);
+  VALIDATE_ONLY();
+  ammon_k_rope p = {q, k_proj, k_cache, (const ammon_k_step *)step, table,
+                    (uint32_t)q_numel, (uint32_t)kv_dim, head, seq, (uint32_t)kv_dtype};
+  return launch(rt, stream, rt->k.rope, cdiv(q_numel / 2, kWorkgroup), 1, 0, p, what);
+}
+
+ammon_status ammon_rope_store(ammon_runtime *rt, ammon_stream stream, float *q,
+                              uint32_t q_heads, const float *k_proj, uint32_t kv_heads,
+                              uint32_t head, void *k_cache, ammon_dtype kv_dtype, uint32_t seq,
+                              const ammon_decode_step *step, const float *table) {
+  AMMON_CHECK(k_proj != nullptr, "rope_store: parameter `k_proj` is NULL");
+  return rope_impl(rt, stream, q, q_heads, k_proj, kv_heads, head, k_cache, kv_dtype, seq, step,
+                   table, "rope_store");
+}
+
+ammon_status ammon_rope(ammon_runtime *rt, ammon_stream stream, float *q, uint32_t q_heads,
+                        uint32_t kv_heads, uint32_t head, void *k_cache, ammon_dtype kv_dtype,
+                        uint32_t seq, const ammon_decode_step *step, const float *table) {
+  return rope_impl(rt, stream, q, q_heads, nullptr, kv_heads, head, k_cache, kv_dtype, seq, step,
+                   table, "rope");
+}
+
+ammon_status ammon_cache_store(ammon_runtime *rt, ammon_stream stream, const float *src,
+                               uint32_t kv_heads, uint32_t head, void *cache,
+                               ammon_dtype kv_dtype, uint32_t seq,
+                               const ammon_decode_step *step) {
+  REQUIRE_RT();
+  AMMON_CHECK(src && cache && step, "cache_store: NULL src, cache or step");
+  AMMON_CHECK(valid_dtype(kv_dtype), "cache_store: unknown dtype %d", (int)kv_dtype);
+  AMMON_CHECK(kv_heads > 0 && head > 0 && seq > 0, "cache_store: empty shape");
+  VALIDATE_ONLY();
+  const uint32_t kv_dim = kv_heads * head;
+  ammon_k_cache_store p = {src, cache, (const ammon_k_step *)step, kv_dim, head, seq,
+                           (uint32_t)kv_dtype};
+  return launch(rt, stream, rt->k.cache_store, cdiv(kv_dim, kWorkgroup), 1, 0, p, "cache_store");
+}
+
+// ---- attention ---------------------------------------------------------------------------
+ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, const float *q,
+                                     uint32_t q_heads, const void *k_cache, const void *v_cache,
+                                     ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head,
+                                     uint32_t seq, const ammon_decode_step *step,
+                                     uint32_t split_len, float *partial) {
+  REQUIRE_RT();
+  AMMON_CHECK(q && k_cache && v_cache && step && partial,
+              "attention_partial: NULL q, cache, step or partial");
+  AMMON_CHECK(valid_dtype(kv_dtype), "attention_partial: unknown kv dtype %d", (int)kv_dtype);
+  ammon_status st = attention_check(rt, "attention_partial", q_heads, kv_heads, head, seq, split_len);
+  if (st != AMMON_OK) return st;
+  const int ci = att_chunk_index(kv_dtype, head, k_cache, v_cache);
+  AMMON_CHECK(ci >= 0, "attention_partial: head %u needs an even width above 64", head);
+  const int gi = att_group_index(q_heads / kv_heads);
+  VALIDATE_ONLY();
+  const uint32_t splits = ammon_attention_splits(seq, split_len);
+  ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, nullptr,
+                         q_heads, kv_heads, head, seq, split_len, splits};
+  const int dt = kv_dtype == AMMON_BF16 ? 1 : 0;
+  return launch(rt, stream, rt->k.att_partial[dt][ci][gi], splits, kv_heads, 0, p,
+                "attention_partial");
+}
+
+ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
+                                     const float *partial, uint32_t q_heads, uint32_t head,
+                                     uint32_t seq, const ammon_decode_step *step,
+                                     uint32_t split_len, float *out) {
+  REQUIRE_RT();
+  AMMON_CHECK(partial && step && out, "attention_combine: NULL partial, step or out");
+  AMMON_CHECK(q_heads > 0 && head > 0 && seq > 0,
+              "attention_combine: empty shape (q_heads=%u, head=%u, seq=%u)", q_heads, head, seq);
+  AMMON_CHECK(head <= AMMON_ATTENTION_MAX_HEAD, "attention_combine: head size %u exceeds %u",
+              head, AMMON_ATTENTION_MAX_HEAD);
+  AMMON_CHECK(split_len >= 1 && split_len <= AMMON_ATTENTION_MAX_SPLIT,
+              "attention_combine: split length %u outside [1, %u]", split_len,
+              AMMON_ATTENTION_MAX_SPLIT);
+  AMMON_CHECK(ammon_attention_splits(seq, split_len) <= AMMON_ATTENTION_MAX_SPLITS,
+              "attention_combine: %u splits exceed %u", ammon_attention_splits(seq, split_len),
+              AMMON_ATTENTION_MAX_SPLITS);
+  VALIDATE_ONLY();
+  ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
+                         out, q_heads, 1, head, seq, split_len,
+                         ammon_attention_splits(seq, split_len)};
+  return launch(rt, stream, rt->k.att_combine, q_heads, 1, 0, p, "attention_combine");
+}
+
+ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, const float *q,
+                                    uint32_t q_heads, const void *k_cache, const void *v_cache,
+                                    ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head,
+                                    uint32_t seq, const ammon_decode_step *step,
+                                    uint32_t split_len, float *partial, size_t partial_bytes,
+                                    float *out) {
+  REQUIRE_RT();
+  AMMON_CHECK(partial_bytes >= ammon_attention_scratch_bytes(q_heads, head, seq, split_len),
+              "attention: partial scratch must be %zu bytes ([%u, %u, %u] fp32)",
+              ammon_attention_scratch_bytes(q_heads, head, seq, split_len), q_heads,
+              ammon_attention_splits(seq, split_len), head + 2);
+  ammon_status st = ammon_attention_partial(rt, AMMON_STREAM_VALIDATE, q, q_heads, k_cache,
+                                            v_cache, kv_dtype, kv_heads, head, seq, step,
+                                            split_len, partial);
+  if (st != AMMON_OK) return st;
+  st = ammon_attention_combine(rt, AMMON_STREAM_VALIDATE, partial, q_heads, head, seq, step,
+                               split_len, out);
+  if (st != AMMON_OK) return st;
+  VALIDATE_ONLY();
+  st = ammon_attention_partial(rt, stream, q, q_heads, k_cache, v_cache, kv_dtype, kv_heads, head,
+                               seq, step, split_len, partial);
+  if (st != AMMON_OK) return st;
+  return ammon_attention_combine(rt, stream, partial, q_heads, head, seq, step, split_len, out);
+}
+
+// ---- elementwise ---------------------------------------------------------------------------
+ammon_status ammon_swiglu(ammon_runtime *rt, ammon_stream stream, float *hb, const float *hb2,
+                          uint32_t n) {
+  REQUIRE_RT();
+  AMMON_CHECK(n == 0 || (hb && hb2), "swiglu: NULL hb or hb2");
+  VALIDATE_ONLY();
+  ammon_k_elementwise p = {hb, nullptr, hb2, n};
+  return launch(rt, stream, rt->k.swiglu, cdiv(n, kWorkgroup), 1, 0, p, "swiglu");
+}
+
+ammon_status ammon_add(ammon_runtime *rt, ammon_stream stream, const float *a, const float *b,
+                       float *out, uint32_t n) {
+  REQUIRE_RT();
+  AMMON_CHECK(n == 0 || (a && b && out), "add: NULL operand");
+  VALIDATE_ONLY();
+  ammon_k_elementwise p = {out, a, b, n};
+  return launch(rt, stream, rt->k.add, cdiv(n, kWorkgroup), 1, 0, p, "add");
+}
+
+// ---- GEMV family ------------------------------------------------------------------------
+ammon_status ammon_gemv(ammon_runtime *rt, ammon_stream stream, const void *w,
+                        ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x, float *y,
+                        const float *residual) {
+  REQUIRE_RT();
+  GemvArgs a = {};
+  a.mode = residual ? AMMON_GEMV_RESIDUAL : AMMON_GEMV_PLAIN;
+  a.w0 = w;
+  a.w_dtype = w_dtype;
+  a.d = d;
+  a.n = n;
+  a.rows = d;
+  a.x = x;
+  a.residual = residual;
+  a.y = y;
+  return gemv_check_and_launch(rt, stream, a, "gemv");
+}
+
+ammon_status ammon_gemv_rmsnorm(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                const void *w, ammon_dtype w_dtype, uint32_t d, uint32_t n,
+                                float *y) {
+  REQUIRE_RT();
+  AMMON_CHECK(norm_weight != nullptr, "gemv_rmsnorm: parameter `norm_weight` is NULL");
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_PLAIN;
+  a.w0 = w;
+  a.w_dtype = w_dtype;
+  a.d = d;
+  a.n = n;
+  a.rows = d;
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = y;
+  return gemv_check_and_launch(rt, stream, a, "gemv_rmsnorm");
+}
+
+ammon_status ammon_qkv_rope_store(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                  const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                  const void *wq, const void *wk, const void *wv,
+                                  ammon_dtype w_dtype, uint32_t dim, uint32_t q_heads,
+                                  uint32_t kv_heads, uint32_t head, float *q, void *k_cache,
+                                  void *v_cache, ammon_dtype kv_dtype, uint32_t seq,
+                                  const ammon_decode_step *step, const float *table) {
+  REQUIRE_RT();
+  AMMON_CHECK(wq && wk && wv, "qkv: NULL wq, wk or wv");
+  AMMON_CHECK(k_cache && v_cache && step && table, "qkv: NULL cache, step or table");
+  AMMON_CHECK(valid_dtype(kv_dtype), "qkv: unknown kv dtype %d", (int)kv_dtype);
+  AMMON_CHECK(head >= 2 && head % 2 == 0, "qkv: head size %u must be even", head);
+  AMMON_CHECK(q_heads > 0 && kv_heads > 0 && seq > 0, "qkv: empty shape");
+  const uint64_t q_dim = (uint64_t)q_heads * head, kv_dim = (uint64_t)kv_heads * head;
+  AMMON_CHECK(kv_dim <= q_dim, "attention: kv width must be even and no wider than q");
+  AMMON_CHECK(q_dim + 2 * kv_dim < (1ull << 31), "qkv: too many rows");
+  AMMON_CHECK(!overlaps(k_cache, (size_t)kv_dim * seq * dsize(kv_dtype), v_cache,
+                        (size_t)kv_dim * seq * dsize(kv_dtype)),
+              "qkv: key and value caches overlap");
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_QKV;
+  a.w0 = wq;
+  a.w1 = wk;
+  a.w2 = wv;
+  a.w_dtype = w_dtype;
+  a.d = (uint32_t)q_dim;
+  a.n = dim;
+  a.rows = (uint32_t)(q_dim + 2 * kv_dim);
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.step = step;
+  a.table = table;
+  a.kv_dim = (uint32_t)kv_dim;
+  a.head = head;
+  a.seq = seq;
+  a.kv_dtype = kv_dtype;
+  return gemv_check_and_launch(rt, stream, a, "qkv_rope_store");
+}
+
+ammon_status ammon_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                  const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                  const void *w1, const void *w3, ammon_dtype w_dtype,
+                                  uint32_t dim, uint32_t hidden, float *hb) {
+  REQUIRE_RT();
+  AMMON_CHECK(w1 && w3, "gate_up_swiglu: NULL w1 or w3");
+  AMMON_CHECK((uint64_t)hidden * 2 < (1ull << 31), "gate_up_swiglu: too many rows");
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_SWIGLU;
+  a.w0 = w1;
+  a.w1 = w3;
+  a.w_dtype = w_dtype;
+  a.d = hidden;
+  a.n = dim;
+  a.rows = 2 * hidden;
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = hb;
+  return gemv_check_and_launch(rt, stream, a, "gate_up_swiglu");
+}
+
+// ---- argmax ---------------------------------------------------------------------------------
+static uint32_t argmax_blocks(uint32_t n) {
+  return std::max<uint32_t>(1, std::min<uint32_t>(256, cdiv(n, (uint64_t)kWorkgroup * 2)));
+}
+
+size_t ammon_argmax_scratch_bytes(uint32_t n) { return (size_t)argmax_blocks(n) * 8; }
+
+static ammon_status argmax_impl(ammon_runtime *rt, ammon_stream stream, const float *logits,
+                                uint32_t n, void *scratch, int32_t *out, const int32_t *prompt,
+                                uint32_t n_prompt, ammon_decode_step *step, int32_t *tokens,
+                                uint32_t max_tokens, const char *what) {
+  REQUIRE_RT();
+  AMMON_CHECK(logits && scratch, "%s: NULL logits or scratch", what);
+  AMMON_CHECK(n > 0, "%s: empty logits", what);
+  VALIDATE_ONLY();
+  const uint32_t blocks = argmax_blocks(n);
+  ammon_k_argmax p = {};
+  p.logits = logits;
+  p.cand_v = (float *)scratch;
+  p.cand_i = (uint32_t *)((char *)scratch + (size_t)blocks * 4);
+  p.out = out;
+  p.step = (ammon_k_step *)step;
+  p.prompt = prompt;
+  p.tokens = tokens;
+  p.n = n;
+  p.blocks = blocks;
+  p.n_prompt = n_prompt;
+  p.max_tokens = max_tokens;
+  ammon_status st = launch(rt, stream, rt->k.argmax_partial, blocks, 1, 0, p, what);
+  if (st != AMMON_OK) return st;
+  return launch(rt, stream, rt->k.argmax_final, 1, 1, 0, p, what);
+}
+
+ammon_status ammon_argmax(ammon_runtime *rt, ammon_stream stream, const float *logits,
+                          uint32_t n, void *scratch, int32_t *out) {
+  AMMON_CHECK(out != nullptr, "argmax: parameter `out` is NULL");
+  return argmax_impl(rt, stream, logits, n, scratch, out, nullptr, 0, nullptr, nullptr, 0,
+                     "argmax");
+}
+
+ammon_status ammon_greedy_next(ammon_runtime *rt, ammon_stream stream, const float *logits,
+                               uint32_t n, void *scratch, const int32_t *prompt,
+                               uint32_t n_prompt, ammon_decode_step *step, int32_t *tokens,
+                               uint32_t max_tokens) {
+  AMMON_CHECK(step != nullptr, "greedy_next: parameter `step` is NULL");
+  AMMON_CHECK(n_prompt == 0 || prompt != nullptr, "greedy_next: NULL prompt");
+  return argmax_impl(rt, stream, logits, n, scratch, nullptr, prompt, n_prompt, step, tokens,
+                     max_tokens, "greedy_next");
+}
+
+// ---- fills -------------------------------------------------------------------------------------
+ammon_status ammon_fill(ammon_runtime *rt, ammon_stream stream, void *dst, ammon_dtype dtype,
+                        size_t count, float value) {
+  REQUIRE_RT();
+  AMMON_CHECK(valid_dtype(dtype), "fill: unknown dtype %d", (int)dtype);
+  AMMON_CHECK(count == 0 || dst, "fill: NULL destination");
+  VALIDATE_ONLY();
+  ammon_k_fill p = {};
+  p.dst = dst;
+  p.count = count;
+  p.dtype = (uint32_t)dtype;
+  if (dtype == AMMON_BF16) {
+    uint32_t u;
+    std::memcpy(&u, &value, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u)
+      p.bits = (u >> 16) | 0x40u;
+    else
+      p.bits = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
+  } else {
+    std::memcpy(&p.bits, &value, 4);
+  }
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(cdiv(count, kWorkgroup),
+                                                     (uint64_t)rt->info.compute_units * 32);
+  return launch(rt, stream, rt->k.fill_const, grid, 1, 0, p, "fill");
+}
+
+ammon_status ammon_fill_normal(ammon_runtime *rt, ammon_stream stream, void *dst,
+                               ammon_dtype dtype, size_t count, uint64_t seed,
+                               uint64_t stream_id, float mean, float std) {
+  REQUIRE_RT();
+  AMMON_CHECK(valid_dtype(dtype), "fill_normal: unknown dtype %d", (int)dtype);
+  AMMON_CHECK(count == 0 || dst, "fill_normal: NULL destination");
+  VALIDATE_ONLY();
+  ammon_k_fill p = {};
+  p.dst = dst;
+  p.count = count;
+  p.seed = seed;
+  p.stream = stream_id;
+  p.mean = mean;
+  p.std = std;
+  p.dtype = (uint32_t)dtype;
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(cdiv((count + 1) / 2, kWorkgroup),
+                                                     (uint64_t)rt->info.compute_units * 32);
+  return launch(rt, stream, rt->k.fill_normal, grid, 1, 0, p, "fill_normal");
+}
+
+}  // extern "C"
