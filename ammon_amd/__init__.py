@@ -12,11 +12,14 @@ from ._abi import (ATTENTION_MAX_HEAD, ATTENTION_SPLIT_REF, BF16, DEFAULT_ROPE_T
 from .runtime import (DeviceBuffer, Runtime, Timer, argmax_scratch_bytes, attention_scratch_bytes,
                       attention_splits, kv_permute, kv_unpermute, rope_table_host, storage_dtype)
 
+from . import model
+from .model import LlamaModel
+
 LIB_PATH = _abi.LIB_PATH
 
 __all__ = [
     "ATTENTION_MAX_HEAD", "ATTENTION_SPLIT_REF", "BF16", "DEFAULT_ROPE_THETA", "F32",
     "AmmonError", "DecodeStep", "DeviceBuffer", "Runtime", "Timer", "argmax_scratch_bytes",
     "attention_scratch_bytes", "attention_splits", "kv_permute", "kv_unpermute",
-    "rope_table_host", "storage_dtype", "LIB_PATH",
+    "rope_table_host", "storage_dtype", "LIB_PATH", "LlamaModel", "model",
 ]

@@ -44,7 +44,8 @@ class DeviceInfo(ctypes.Structure):
                 ("name", ctypes.c_char * 128)]
 
 
-# name -> (restype, argtypes).  Keep in the order of include/ammon/ammon.h.
+# name -> (restype, argtypes), in the order of include/ammon/ammon.h, then
+# include/ammon/ammon_model.h.
 SIGNATURES = {
     "ammon_runtime_create": (_ST, [ctypes.c_int, ctypes.POINTER(_P)]),
     "ammon_runtime_release": (_ST, [_P]),
@@ -64,6 +65,10 @@ SIGNATURES = {
     "ammon_event_record": (_ST, [_P, _P, _P]),
     "ammon_event_synchronize": (_ST, [_P, _P]),
     "ammon_event_elapsed_ms": (_ST, [_P, _P, _P, ctypes.POINTER(_F)]),
+    "ammon_capture_begin": (_ST, [_P, _P]),
+    "ammon_capture_end": (_ST, [_P, _P, ctypes.POINTER(_P)]),
+    "ammon_graph_launch": (_ST, [_P, _P, _P]),
+    "ammon_graph_destroy": (_ST, [_P, _P]),
     "ammon_fill": (_ST, [_P, _P, _P, _DT, _SZ, _F]),
     "ammon_fill_normal": (_ST, [_P, _P, _P, _DT, _SZ, _U64, _U64, _F, _F]),
     "ammon_rope_table_bytes": (_SZ, [_U32, _U32]),
@@ -87,6 +92,7 @@ SIGNATURES = {
     "ammon_swiglu": (_ST, [_P, _P, _P, _P, _U32]),
     "ammon_add": (_ST, [_P, _P, _P, _P, _P, _U32]),
     "ammon_gemv": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _P, _P]),
+    "ammon_gemv_at_position": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _P, _U32, _P]),
     "ammon_gemv_rmsnorm": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _DT, _U32, _U32, _P]),
     "ammon_qkv_rope_store": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _P, _DT, _U32, _U32, _U32,
                                    _U32, _P, _P, _P, _DT, _U32, _P, _P]),
@@ -95,6 +101,40 @@ SIGNATURES = {
     "ammon_argmax": (_ST, [_P, _P, _P, _U32, _P, _P]),
     "ammon_greedy_next": (_ST, [_P, _P, _P, _U32, _P, _P, _U32, _P, _P, _U32]),
 }
+
+
+class LlamaConfig(ctypes.Structure):
+    """ammon_llama_config (include/ammon/ammon_model.h)."""
+    _fields_ = [("dim", _U32), ("n_layers", _U32), ("n_heads", _U32), ("n_kv_heads", _U32),
+                ("hidden", _U32), ("vocab", _U32), ("max_seq", _U32), ("theta", _F),
+                ("eps", _F), ("w_dtype", ctypes.c_int), ("kv_dtype", ctypes.c_int),
+                ("use_graph", _U32), ("split_len", _U32)]
+
+
+class LlamaWeights(ctypes.Structure):
+    """ammon_llama_weights: device pointers, stacked per layer."""
+    _fields_ = [(n, _P) for n in ("tok_emb", "rms_att", "rms_ffn", "wq", "wk", "wv", "wo",
+                                  "w1", "w2", "w3", "rms_final", "wcls")]
+
+
+SIGNATURES.update({
+    "ammon_llama_create": (_ST, [_P, ctypes.POINTER(LlamaConfig), ctypes.POINTER(LlamaWeights),
+                                 ctypes.POINTER(_P)]),
+    "ammon_llama_destroy": (_ST, [_P]),
+    "ammon_llama_step": (_ST, [_P, _U32, _U32, _P]),
+    "ammon_llama_generate_tokens": (_ST, [_P, _P, _U32, _U32, ctypes.c_int, _I32, _P,
+                                          ctypes.POINTER(_U32), ctypes.POINTER(ctypes.c_double),
+                                          _P]),
+    "ammon_llama_generate_tokens_device": (_ST, [_P, _P, _U32, _U32, ctypes.c_int, _I32, _P,
+                                                 ctypes.POINTER(_U32),
+                                                 ctypes.POINTER(ctypes.c_double), _P]),
+    "ammon_llama_decode": (_ST, [_P, _U32, _U32, _U32, _P]),
+    "ammon_llama_tokens": (_ST, [_P, _U32, _U32, _P]),
+    "ammon_llama_kv_layer": (_ST, [_P, _U32, ctypes.POINTER(_P), ctypes.POINTER(_P)]),
+    "ammon_llama_stream": (_ST, [_P, ctypes.POINTER(_P)]),
+    "ammon_llama_logits": (_ST, [_P, ctypes.POINTER(_P)]),
+    "ammon_llama_launches": (_ST, [_P, ctypes.POINTER(_U32)]),
+})
 
 
 class AmmonError(RuntimeError):

@@ -1,0 +1,412 @@
+// llama.cpp -- the llama2.c-convention test model built from the C++ modules,
+// and its C entry points (include/ammon/ammon_model.h).
+//
+// Graph (the one Ammon's modules imply; the reference leaves it to
+// architecture crates, README.md:5):
+//   x = embed(token)
+//   per layer: CausalAttentionBlock (x += attn), SwiGluBlock (x += ffn)
+//   logits = Wcls . rmsnorm(x, w_final)          (one fused launch)
+// One token is recorded once into a Scheme and replayed as a HIP graph; the
+// DecodeStep parcel is the only per-token input.  A second scheme appends the
+// device greedy step (argmax + prompt forcing + DecodeStep update) so tokens
+// can be generated back to back without host round trips.
+#include <algorithm>
+#include <cstring>
+#include <memory>
+
+#include "../runtime/internal.h"
+#include "ammon/ammon.hpp"
+#include "ammon/ammon_model.h"
+
+namespace ammon {
+namespace {
+
+class LlamaModel : public AutoregressiveModel {
+ public:
+  LlamaModel(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w);
+  ~LlamaModel() override;
+
+  size_t vocab_size() const override { return c_.vocab; }
+  uint32_t max_seq_len() const override { return c_.max_seq; }
+  const std::vector<float> &step(uint32_t token, uint32_t pos) override;
+
+  GenerateTokenOutput generate_device(const std::vector<int32_t> &prompt, uint32_t max_new,
+                                      std::optional<int32_t> stop_on, float *last_logits);
+  void decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, int32_t *tokens);
+  KvLayer kv_layer(uint32_t l) const { return cache_.layer(l); }
+  void read_tokens(uint32_t start, uint32_t n, int32_t *out);
+  ammon_stream stream() const { return stream_; }
+  float *device_logits() const { return (float *)logits_.data(); }
+  uint32_t launches() const { return (uint32_t)token_scheme_->ir_node_count(); }
+  // Host logits of the most recent step() (what generate_tokens last saw).
+  const std::vector<float> &last_logits() const { return host_logits_; }
+
+ private:
+  void record_token(Scheme &s);
+  void ensure_decode_scheme(uint32_t n_prompt);
+  void deposit(uint32_t token, uint32_t pos, ammon_stream stream);
+
+  Runtime rt_;
+  ammon_llama_config c_;
+  uint32_t head_, q_dim_, kv_dim_;
+  TensorView tok_emb_, rms_final_, wcls_;
+  std::vector<CausalAttentionBlockWeights> attn_w_;
+  std::vector<SwiGluBlockWeights> ffn_w_;
+  Embedding embed_;
+  CausalAttentionBlock attn_;
+  SwiGluBlock ffn_;
+  Linear lm_head_;
+  KvCache cache_;
+  Tensor x_, logits_, step_, prompt_, tokens_, scratch_;
+  ammon_stream stream_ = nullptr;  // both schemes replay here, in order
+  std::unique_ptr<Scheme> token_scheme_, decode_scheme_;
+  uint32_t decode_prompt_ = 0xffffffffu;
+  ammon_decode_step *pinned_step_ = nullptr;
+  float *pinned_logits_ = nullptr;
+  std::vector<float> host_logits_;
+};
+
+DType dt(ammon_dtype d) { return (DType)d; }
+
+TensorView view(const void *base, DType d, size_t layer, std::vector<uint32_t> dims) {
+  Shape s = Shape::from_dims(std::move(dims));
+  return TensorView((char *)base + layer * s.numel() * dtype_size(d), s, d);
+}
+
+AttentionOptions attention_options(const ammon_llama_config &c) {
+  AttentionOptions o;
+  o.theta = c.theta;
+  o.eps = c.eps;
+  o.split_len = c.split_len;
+  return o;
+}
+
+uint32_t checked_head(const ammon_llama_config &c) {
+  if (c.n_heads == 0 || c.dim % c.n_heads != 0)
+    throw Error(AMMON_E_VALIDATION, "llama: dim is not divisible by n_heads");
+  if (c.n_kv_heads == 0 || c.n_heads % c.n_kv_heads != 0)
+    throw Error(AMMON_E_VALIDATION, "llama: n_heads is not a multiple of n_kv_heads");
+  if (c.vocab == 0 || c.max_seq == 0 || c.n_layers == 0 || c.hidden == 0)
+    throw Error(AMMON_E_VALIDATION, "llama: empty configuration");
+  return c.dim / c.n_heads;
+}
+
+LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w)
+    : rt_(rt),
+      c_(c),
+      head_(checked_head(c)),
+      q_dim_(head_ * c.n_heads),
+      kv_dim_(head_ * c.n_kv_heads),
+      embed_(rt),
+      attn_(rt, c.dim, c.n_heads, c.max_seq, attention_options(c)),
+      ffn_(rt, c.dim, c.hidden, c.eps),
+      lm_head_(rt),
+      cache_(rt, c.n_layers, c.max_seq, c.n_kv_heads, head_, dt(c.kv_dtype)) {
+  const DType wd = dt(c.w_dtype);
+  if (!w.tok_emb || !w.rms_att || !w.rms_ffn || !w.wq || !w.wk || !w.wv || !w.wo || !w.w1 ||
+      !w.w2 || !w.w3 || !w.rms_final || !w.wcls)
+    throw Error(AMMON_E_VALIDATION, "llama: a weight pointer is NULL");
+  tok_emb_ = view(w.tok_emb, wd, 0, {c.vocab, c.dim});
+  rms_final_ = view(w.rms_final, DType::F32, 0, {c.dim});
+  wcls_ = view(w.wcls, wd, 0, {c.vocab, c.dim});
+  for (uint32_t l = 0; l < c.n_layers; ++l) {
+    attn_w_.push_back(CausalAttentionBlockWeights{
+        view(w.rms_att, DType::F32, l, {c.dim}), view(w.wq, wd, l, {q_dim_, c.dim}),
+        view(w.wk, wd, l, {kv_dim_, c.dim}), view(w.wv, wd, l, {kv_dim_, c.dim}),
+        view(w.wo, wd, l, {c.dim, q_dim_})});
+    ffn_w_.push_back(SwiGluBlockWeights{
+        view(w.rms_ffn, DType::F32, l, {c.dim}), view(w.w1, wd, l, {c.hidden, c.dim}),
+        view(w.w3, wd, l, {c.hidden, c.dim}), view(w.w2, wd, l, {c.dim, c.hidden})});
+  }
+  x_ = Tensor::zeros(rt, Shape::vector(c.dim), DType::F32);
+  logits_ = Tensor::zeros(rt, Shape::vector(c.vocab), DType::F32);
+  step_ = DecodeStep::parcel(rt);
+  prompt_ = Tensor::zeros(rt, Shape::vector(c.max_seq), DType::I32);
+  tokens_ = Tensor::zeros(rt, Shape::vector(c.max_seq), DType::I32);
+  scratch_ = Tensor::zeros(rt, Shape::vector((uint32_t)(ammon_argmax_scratch_bytes(c.vocab) / 4)),
+                           DType::F32);
+  check(ammon_alloc_host(rt.raw(), sizeof(ammon_decode_step), (void **)&pinned_step_), "llama");
+  check(ammon_alloc_host(rt.raw(), sizeof(float) * c.vocab, (void **)&pinned_logits_), "llama");
+  host_logits_.resize(c.vocab);
+  check(ammon_stream_create(rt.raw(), &stream_), "llama stream");
+  token_scheme_ = std::make_unique<Scheme>(rt, c.use_graph != 0, stream_);
+  record_token(*token_scheme_);
+}
+
+LlamaModel::~LlamaModel() {
+  decode_scheme_.reset();
+  token_scheme_.reset();
+  if (stream_) ammon_stream_destroy(rt_.raw(), stream_);
+  if (pinned_step_) ammon_free_host(rt_.raw(), pinned_step_);
+  if (pinned_logits_) ammon_free_host(rt_.raw(), pinned_logits_);
+}
+
+void LlamaModel::record_token(Scheme &s) {
+  embed_.record(s, tok_emb_, step_, x_.view());
+  for (uint32_t l = 0; l < c_.n_layers; ++l) {
+    const std::string layer = "layer" + std::to_string(l);
+    attn_.record_group(s, layer + "/attn", x_.view(), attn_w_[l], cache_.layer(l), step_);
+    ffn_.record_group(s, layer + "/ffn", x_.view(), ffn_w_[l]);
+  }
+  lm_head_.record_normed(s, wcls_, x_.view(), rms_final_, logits_.view(), c_.eps);
+}
+
+void LlamaModel::ensure_decode_scheme(uint32_t n_prompt) {
+  if (decode_scheme_ && decode_prompt_ == n_prompt) return;
+  auto s = std::make_unique<Scheme>(rt_, c_.use_graph != 0, stream_);
+  record_token(*s);
+  kernels::greedy_next(*s, "greedy_next", logits_.view(), scratch_.view(), prompt_.view(), n_prompt,
+                       step_, tokens_.view());
+  decode_scheme_ = std::move(s);
+  decode_prompt_ = n_prompt;
+}
+
+void LlamaModel::deposit(uint32_t token, uint32_t pos, ammon_stream stream) {
+  // The pinned staging slot is reused per token: wait for the previous
+  // deposit on this stream before overwriting it.
+  check(ammon_stream_synchronize(rt_.raw(), stream), "deposit");
+  pinned_step_->token = token;
+  pinned_step_->position = pos;
+  check(ammon_memcpy(rt_.raw(), step_.data(), pinned_step_, sizeof(ammon_decode_step),
+                     AMMON_COPY_H2D, stream),
+        "deposit");
+}
+
+const std::vector<float> &LlamaModel::step(uint32_t token, uint32_t pos) {
+  if (token >= c_.vocab)
+    throw Error(AMMON_E_VALIDATION, "step: token " + std::to_string(token) + " >= vocab " +
+                                        std::to_string(c_.vocab));
+  if (pos >= c_.max_seq)
+    throw Error(AMMON_E_VALIDATION, "step: position " + std::to_string(pos) + " >= max_seq " +
+                                        std::to_string(c_.max_seq));
+  Scheme &s = *token_scheme_;
+  deposit(token, pos, s.stream());
+  s.submit();
+  check(ammon_memcpy(rt_.raw(), pinned_logits_, logits_.data(), sizeof(float) * c_.vocab,
+                     AMMON_COPY_D2H, s.stream()),
+        "logits");
+  s.synchronize();
+  std::memcpy(host_logits_.data(), pinned_logits_, sizeof(float) * c_.vocab);
+  return host_logits_;
+}
+
+GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prompt,
+                                                uint32_t max_new, std::optional<int32_t> stop_on,
+                                                float *last_logits) {
+  if (prompt.empty()) throw Error(AMMON_E_VALIDATION, "expected at least one prompt token");
+  for (int32_t t : prompt)
+    if (t < 0 || (uint32_t)t >= c_.vocab)
+      throw Error(AMMON_E_VALIDATION, "prompt token " + std::to_string(t) + " outside the vocab");
+  const uint32_t limit = std::min(max_new, c_.max_seq);
+  const uint32_t steps = limit > 0 ? limit - 1 : 0;
+  const uint32_t n_prompt = (uint32_t)std::min<size_t>(prompt.size(), c_.max_seq);
+  ensure_decode_scheme(n_prompt);
+  Scheme &s = *decode_scheme_;
+  check(ammon_memcpy(rt_.raw(), prompt_.data(), prompt.data(), sizeof(int32_t) * n_prompt,
+                     AMMON_COPY_H2D, s.stream()),
+        "prompt upload");
+  deposit((uint32_t)prompt[0], 0, s.stream());
+  ammon_event e0 = nullptr, e1 = nullptr;
+  check(ammon_event_create(rt_.raw(), &e0), "event");
+  check(ammon_event_create(rt_.raw(), &e1), "event");
+  for (uint32_t i = 0; i < steps; ++i) {
+    s.submit();
+    if (i == 0) check(ammon_event_record(rt_.raw(), e0, s.stream()), "event");
+  }
+  check(ammon_event_record(rt_.raw(), e1, s.stream()), "event");
+  s.synchronize();
+  float ms = 0.f;
+  if (steps > 1) check(ammon_event_elapsed_ms(rt_.raw(), e0, e1, &ms), "event");
+  ammon_event_destroy(rt_.raw(), e0);
+  ammon_event_destroy(rt_.raw(), e1);
+
+  std::vector<int32_t> all(steps);
+  if (steps)
+    check(ammon_memcpy(rt_.raw(), all.data(), tokens_.data(), sizeof(int32_t) * steps,
+                       AMMON_COPY_D2H, s.stream()),
+          "tokens");
+  if (last_logits)
+    check(ammon_memcpy(rt_.raw(), last_logits, logits_.data(), sizeof(float) * c_.vocab,
+                       AMMON_COPY_D2H, s.stream()),
+          "logits");
+  s.synchronize();
+  GenerateTokenOutput out;
+  out.prompt_tokens = prompt.size();
+  for (int32_t t : all) {
+    if (stop_on && *stop_on == t) break;
+    out.tokens.push_back(t);
+  }
+  out.tokens_per_second = (steps > 1 && ms > 0.f) ? (double)(steps - 1) / (ms * 1e-3) : 0.0;
+  return out;
+}
+
+void LlamaModel::decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, int32_t *tokens) {
+  if (token >= c_.vocab) throw Error(AMMON_E_VALIDATION, "decode: token outside the vocab");
+  if ((uint64_t)start_pos + n_steps > c_.max_seq)
+    throw Error(AMMON_E_VALIDATION, "decode: start_pos + n_steps exceeds max_seq");
+  ensure_decode_scheme(0);
+  Scheme &s = *decode_scheme_;
+  deposit(token, start_pos, s.stream());
+  for (uint32_t i = 0; i < n_steps; ++i) s.submit();
+  if (tokens) {
+    check(ammon_memcpy(rt_.raw(), tokens, (int32_t *)tokens_.data() + start_pos,
+                       sizeof(int32_t) * n_steps, AMMON_COPY_D2H, s.stream()),
+          "tokens");
+    s.synchronize();
+  }
+}
+
+void LlamaModel::read_tokens(uint32_t start, uint32_t n, int32_t *out) {
+  if ((uint64_t)start + n > c_.max_seq)
+    throw Error(AMMON_E_VALIDATION, "tokens: range exceeds max_seq");
+  check(ammon_stream_synchronize(rt_.raw(), stream_), "tokens");
+  if (!n) return;
+  check(ammon_memcpy(rt_.raw(), out, (int32_t *)tokens_.data() + start, sizeof(int32_t) * n,
+                     AMMON_COPY_D2H, stream_),
+        "tokens");
+  check(ammon_stream_synchronize(rt_.raw(), stream_), "tokens");
+}
+
+}  // namespace
+}  // namespace ammon
+
+// ---- C entry points -------------------------------------------------------------------------
+struct ammon_llama {
+  std::unique_ptr<ammon::LlamaModel> model;
+  ammon::Runtime rt;
+};
+
+namespace {
+
+template <typename F>
+ammon_status guarded(F &&fn) {
+  try {
+    fn();
+    return AMMON_OK;
+  } catch (const ammon::Error &e) {
+    return ammon_rt::set_error(e.status(), "%s", e.what());
+  } catch (const std::exception &e) {
+    return ammon_rt::set_error(AMMON_E_HIP, "%s", e.what());
+  }
+}
+
+// The C++ layer holds its own runtime reference for the model's lifetime.
+ammon::Runtime runtime_for(ammon_runtime *rt) {
+  return ammon::Runtime::create(rt->device);
+}
+
+}  // namespace
+
+extern "C" {
+
+ammon_status ammon_llama_create(ammon_runtime *rt, const ammon_llama_config *cfg,
+                                const ammon_llama_weights *w, ammon_llama **out) {
+  AMMON_CHECK(rt && cfg && w && out, "llama_create: NULL argument");
+  return guarded([&] {
+    auto *m = new ammon_llama();
+    try {
+      m->rt = runtime_for(rt);
+      m->model = std::make_unique<ammon::LlamaModel>(m->rt, *cfg, *w);
+    } catch (...) {
+      delete m;
+      throw;
+    }
+    *out = m;
+  });
+}
+
+ammon_status ammon_llama_destroy(ammon_llama *m) {
+  delete m;
+  return AMMON_OK;
+}
+
+ammon_status ammon_llama_step(ammon_llama *m, uint32_t token, uint32_t pos, float *logits) {
+  AMMON_CHECK(m && logits, "llama_step: NULL argument");
+  return guarded([&] {
+    const std::vector<float> &l = m->model->step(token, pos);
+    std::memcpy(logits, l.data(), l.size() * sizeof(float));
+  });
+}
+
+static ammon_status fill_output(const ammon::GenerateTokenOutput &o, int32_t *out_tokens,
+                                uint32_t *n_out, double *tps) {
+  std::copy(o.tokens.begin(), o.tokens.end(), out_tokens);
+  *n_out = (uint32_t)o.tokens.size();
+  if (tps) *tps = o.tokens_per_second;
+  return AMMON_OK;
+}
+
+ammon_status ammon_llama_generate_tokens(ammon_llama *m, const int32_t *prompt, uint32_t n_prompt,
+                                         uint32_t max_new_tokens, int has_stop, int32_t stop_on,
+                                         int32_t *out_tokens, uint32_t *n_out,
+                                         double *tokens_per_second, float *last_logits) {
+  AMMON_CHECK(m && out_tokens && n_out, "llama_generate_tokens: NULL argument");
+  AMMON_CHECK(n_prompt > 0 && prompt, "expected at least one prompt token");
+  return guarded([&] {
+    std::vector<int32_t> p(prompt, prompt + n_prompt);
+    for (int32_t t : p)
+      if (t < 0 || (size_t)t >= m->model->vocab_size())
+        throw ammon::Error(AMMON_E_VALIDATION, "prompt token outside the vocab");
+    auto o = ammon::generate_tokens(*m->model, p, max_new_tokens,
+                                    has_stop ? std::optional<int32_t>(stop_on) : std::nullopt);
+    if (last_logits && !m->model->last_logits().empty())
+      std::memcpy(last_logits, m->model->last_logits().data(),
+                  m->model->last_logits().size() * sizeof(float));
+    fill_output(o, out_tokens, n_out, tokens_per_second);
+  });
+}
+
+ammon_status ammon_llama_generate_tokens_device(ammon_llama *m, const int32_t *prompt,
+                                                uint32_t n_prompt, uint32_t max_new_tokens,
+                                                int has_stop, int32_t stop_on,
+                                                int32_t *out_tokens, uint32_t *n_out,
+                                                double *tokens_per_second, float *last_logits) {
+  AMMON_CHECK(m && out_tokens && n_out, "llama_generate_tokens_device: NULL argument");
+  AMMON_CHECK(n_prompt > 0 && prompt, "expected at least one prompt token");
+  return guarded([&] {
+    std::vector<int32_t> p(prompt, prompt + n_prompt);
+    auto o = m->model->generate_device(
+        p, max_new_tokens, has_stop ? std::optional<int32_t>(stop_on) : std::nullopt, last_logits);
+    fill_output(o, out_tokens, n_out, tokens_per_second);
+  });
+}
+
+ammon_status ammon_llama_decode(ammon_llama *m, uint32_t token, uint32_t start_pos,
+                                uint32_t n_steps, int32_t *tokens) {
+  AMMON_CHECK(m != nullptr, "llama_decode: NULL model");
+  return guarded([&] { m->model->decode(token, start_pos, n_steps, tokens); });
+}
+
+ammon_status ammon_llama_tokens(ammon_llama *m, uint32_t start, uint32_t n, int32_t *tokens) {
+  AMMON_CHECK(m && (tokens || n == 0), "llama_tokens: NULL argument");
+  return guarded([&] { m->model->read_tokens(start, n, tokens); });
+}
+
+ammon_status ammon_llama_kv_layer(ammon_llama *m, uint32_t layer, void **key, void **value) {
+  AMMON_CHECK(m && key && value, "llama_kv_layer: NULL argument");
+  return guarded([&] {
+    ammon::KvLayer l = m->model->kv_layer(layer);
+    *key = l.key.data();
+    *value = l.value.data();
+  });
+}
+
+ammon_status ammon_llama_stream(ammon_llama *m, ammon_stream *stream) {
+  AMMON_CHECK(m && stream, "llama_stream: NULL argument");
+  *stream = m->model->stream();
+  return AMMON_OK;
+}
+
+ammon_status ammon_llama_logits(ammon_llama *m, float **device_logits) {
+  AMMON_CHECK(m && device_logits, "llama_logits: NULL argument");
+  *device_logits = m->model->device_logits();
+  return AMMON_OK;
+}
+
+ammon_status ammon_llama_launches(ammon_llama *m, uint32_t *n) {
+  AMMON_CHECK(m && n, "llama_launches: NULL argument");
+  *n = m->model->launches();
+  return AMMON_OK;
+}
+
+}  // extern "C"

@@ -16,7 +16,7 @@
 // MFMA: at batch 1 the arithmetic intensity is ~1 flop/byte.
 //
 // Modes (virtual rows):
-//   PLAIN     y[r] = dot_r
+//   PLAIN     y[r] = dot_r; with a step, y[position * d + r] (reference gemv)
 //   RESIDUAL  y[r] = residual[r] + dot_r            (y may alias residual)
 //   SWIGLU    rows interleave gate (w0) and up (w1): r = 2i -> gate row i,
 //             r = 2i+1 -> up row i; y[i] = silu(gate) * up in the reference's
@@ -27,9 +27,9 @@
 //             (src/kernels.rs:174-226).
 #include "device_common.h"
 
-// Sum of squares of the staged row, with the same per-lane chunking and
-// reduction order as ammon_rmsnorm so the prologue's normalised x matches
-// the standalone kernel bit for bit.
+// The RMSNorm prologue sums squares with the same per-lane chunking and
+// reduction order as ammon_rmsnorm, so its normalised x matches the
+// standalone kernel bit for bit when the row is 16-byte aligned.
 template <typename WT, int CH, int RPW, int MODE>
 AMMON_DEV void gemv_body(const ammon_k_gemv &p) {
   constexpr int U = (CH >= 4) ? (16 / RPW > 0 ? 16 / RPW : 1) : 4;
@@ -73,6 +73,15 @@ AMMON_DEV void gemv_body(const ammon_k_gemv &p) {
   const uint32_t nch = n / CH;
   uint32_t pos = 0;
   if (MODE == AMMON_GEMV_QKV) pos = p.step->position;
+  // PLAIN with a step: the reference's position-strided gemv
+  // (src/kernels.rs:49-73) writes row `position` of a [seq, d] output.
+  float *yout = p.y;
+  bool write_ok = true;
+  if (MODE == AMMON_GEMV_PLAIN && p.step) {
+    const uint32_t ps = p.step->position;
+    write_ok = ps < p.seq;
+    yout = p.y + (size_t)(write_ok ? ps : 0) * p.d;
+  }
 
   for (uint32_t blk = blockIdx.x; blk < p.row_blocks; blk += gridDim.x) {
     const uint32_t r0 = (blk * AMMON_WAVES + wave) * RPW;
@@ -147,8 +156,8 @@ AMMON_DEV void gemv_body(const ammon_k_gemv &p) {
         if ((uint32_t)k == lane && vr < p.rows) {
           if (MODE == AMMON_GEMV_RESIDUAL)
             p.y[vr] = p.residual[vr] + acc[k];
-          else
-            p.y[vr] = acc[k];
+          else if (write_ok)
+            yout[vr] = acc[k];
         }
       }
     } else if (MODE == AMMON_GEMV_SWIGLU) {

@@ -390,6 +390,28 @@ ammon_status ammon_gemv(ammon_runtime *rt, ammon_stream stream, const void *w,
   return gemv_check_and_launch(rt, stream, a, "gemv");
 }
 
+ammon_status ammon_gemv_at_position(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                    ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                    float *xout, uint32_t seq, const ammon_decode_step *step) {
+  REQUIRE_RT();
+  AMMON_CHECK(step != nullptr, "gemv_at_position: parameter `step` is NULL");
+  AMMON_CHECK(seq > 0, "gemv_at_position: `seq` is 0");
+  AMMON_CHECK(!overlaps(x, (size_t)n * 4, xout, (size_t)seq * d * 4),
+              "gemv_at_position: xout overlaps x");
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_PLAIN;
+  a.w0 = w;
+  a.w_dtype = w_dtype;
+  a.d = d;
+  a.n = n;
+  a.rows = d;
+  a.x = x;
+  a.y = xout;
+  a.step = step;
+  a.seq = seq;
+  return gemv_check_and_launch(rt, stream, a, "gemv_at_position");
+}
+
 ammon_status ammon_gemv_rmsnorm(ammon_runtime *rt, ammon_stream stream, const float *x,
                                 const void *norm_weight, ammon_dtype norm_dtype, float eps,
                                 const void *w, ammon_dtype w_dtype, uint32_t d, uint32_t n,

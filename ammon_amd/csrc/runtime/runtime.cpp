@@ -320,6 +320,53 @@ ammon_status ammon_event_elapsed_ms(ammon_runtime *rt, ammon_event start, ammon_
   return AMMON_OK;
 }
 
+// ---- launch-list capture -------------------------------------------------------
+
+struct GraphHandle {
+  hipGraph_t graph = nullptr;
+  hipGraphExec_t exec = nullptr;
+};
+
+ammon_status ammon_capture_begin(ammon_runtime *rt, ammon_stream stream) {
+  AMMON_CHECK(rt != nullptr, "capture_begin: runtime is NULL");
+  AMMON_CHECK(stream != AMMON_STREAM_VALIDATE, "capture_begin: validate-only stream");
+  AMMON_HIP(hipSetDevice(rt->device));
+  AMMON_HIP(hipStreamBeginCapture(pick(rt, stream), hipStreamCaptureModeThreadLocal));
+  return AMMON_OK;
+}
+
+ammon_status ammon_capture_end(ammon_runtime *rt, ammon_stream stream, ammon_graph *out) {
+  AMMON_CHECK(rt && out, "capture_end: NULL argument");
+  AMMON_CHECK(stream != AMMON_STREAM_VALIDATE, "capture_end: validate-only stream");
+  GraphHandle *g = new GraphHandle();
+  hipError_t e = hipStreamEndCapture(pick(rt, stream), &g->graph);
+  if (e == hipSuccess) e = hipGraphInstantiate(&g->exec, g->graph, nullptr, nullptr, 0);
+  if (e != hipSuccess) {
+    if (g->graph) (void)hipGraphDestroy(g->graph);
+    delete g;
+    return hip_error(e, "capture_end");
+  }
+  *out = (ammon_graph)g;
+  return AMMON_OK;
+}
+
+ammon_status ammon_graph_launch(ammon_runtime *rt, ammon_graph graph, ammon_stream stream) {
+  AMMON_CHECK(rt && graph, "graph_launch: NULL argument");
+  AMMON_CHECK(stream != AMMON_STREAM_VALIDATE, "graph_launch: validate-only stream");
+  AMMON_HIP(hipGraphLaunch(((GraphHandle *)graph)->exec, pick(rt, stream)));
+  return AMMON_OK;
+}
+
+ammon_status ammon_graph_destroy(ammon_runtime *rt, ammon_graph graph) {
+  AMMON_CHECK(rt != nullptr, "graph_destroy: runtime is NULL");
+  if (!graph) return AMMON_OK;
+  GraphHandle *g = (GraphHandle *)graph;
+  if (g->exec) (void)hipGraphExecDestroy(g->exec);
+  if (g->graph) (void)hipGraphDestroy(g->graph);
+  delete g;
+  return AMMON_OK;
+}
+
 // ---- host utilities ----------------------------------------------------------
 
 size_t ammon_rope_table_bytes(uint32_t head, uint32_t seq) {

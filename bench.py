@@ -1,0 +1,326 @@
+"""Decode benchmark: Llama-3-8B-shaped bf16 greedy decode at context 8192.
+
+One step = one full decode token (embed, 32 x [attention block, SwiGLU
+block], final norm + LM head, device argmax feeding the next DecodeStep),
+replayed as a HIP graph with no host round trip.  The KV cache is prefilled
+with N(0, 1) values so every timed token attends over ~8k positions; weights
+are random N(0, 0.02) bf16 generated on the device (synthetic data).
+
+Prints one JSON line (rank 0, N=1 only): decode tokens/s, the dominant
+kernel's HBM roofline from HIP-event timings taken in this run, a per-kernel
+table, and the CPU oracle timed on the host on a bounded sample of the same
+workload (with a greedy-token parity check against the GPU).
+"""
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "decode tokens/sec @ Llama-3-8B shape ctx 8192; kernel HBM GB/s vs peak"
+HBM_PEAK_GBS = 8000.0
+
+LLAMA3_8B = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, hidden=14336, vocab=128256,
+                 max_seq=8192, theta=500000.0, eps=1e-5)
+
+
+class Cfg:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def token_bytes(c, ctx):
+    """Algorithmic HBM bytes of one decode token at context `ctx` (bf16
+    weights and KV, fp32 activations; scratch excluded)."""
+    head = c.dim // c.n_heads
+    q, kv = head * c.n_heads, head * c.n_kv_heads
+    per_layer_w = (q + 2 * kv) * c.dim + c.dim * q + 3 * c.hidden * c.dim
+    weights = 2 * (c.n_layers * per_layer_w + c.vocab * c.dim)
+    kv_read = c.n_layers * 2 * ctx * kv * 2
+    return weights + kv_read
+
+
+def kernel_bytes(c, ctx):
+    """Algorithmic bytes per launch of each per-layer kernel (GEMV: d*n*2 +
+    4n + 4d [+ 4d residual]; attention: 2*ctx*kv_dim*2 + q and out)."""
+    head = c.dim // c.n_heads
+    q, kv = head * c.n_heads, head * c.n_kv_heads
+    return {
+        "gate_up_swiglu": 2 * c.hidden * c.dim * 2 + 4 * c.dim * 2 + 4 * c.hidden,
+        "qkv_rope_store": (q + 2 * kv) * c.dim * 2 + 4 * c.dim * 2 + 4 * q + 2 * 2 * kv,
+        "w2_residual": c.dim * c.hidden * 2 + 4 * c.hidden + 4 * c.dim * 2,
+        "wo_residual": c.dim * q * 2 + 4 * q + 4 * c.dim * 2,
+        "attention_partial": 2 * ctx * kv * 2 + 4 * q,
+        "lm_head": c.vocab * c.dim * 2 + 4 * c.dim * 2 + 4 * c.vocab,
+    }
+
+
+def time_kernels(rt, model, c, weights, ctx, reps):
+    """Average duration of each fused kernel, from HIP events around every
+    launch on the model's stream, cycling through all layers' weights so
+    nothing is served from cache."""
+    import ammon_amd
+    from ammon_amd import Timer
+    from ammon_amd._abi import BF16, F32, call
+
+    L, head = c.n_layers, c.dim // c.n_heads
+    q, kv = head * c.n_heads, head * c.n_kv_heads
+    stream = model.stream
+    x = rt.alloc(c.dim * 4)
+    rt.fill_normal(x, F32, c.dim, 5, 900)
+    qb, hb, xb = rt.alloc(q * 4), rt.alloc(c.hidden * 4), rt.alloc(q * 4)
+    xr = rt.alloc(c.dim * 4)
+    logits = rt.alloc(c.vocab * 4)
+    step = rt.step(1, ctx - 1)
+    table = rt.upload(ammon_amd.rope_table_host(c.theta, head, c.max_seq))
+    split = int(ammon_amd._abi.lib.ammon_attention_default_split(rt.handle, kv, c.max_seq))
+    part = rt.alloc(ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split))
+    rt.synchronize()
+
+    def w(name, l, per):
+        return ctypes.c_void_p(int(weights[name]) + l * per * 2)
+
+    def kv_ptr(l):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        call("ammon_llama_kv_layer", model.handle, l, ctypes.byref(k), ctypes.byref(v))
+        return k, v
+
+    rms = lambda name, l: ctypes.c_void_p(int(weights[name]) + l * c.dim * 4)
+    launches = {
+        "qkv_rope_store": lambda l: call(
+            "ammon_qkv_rope_store", rt.handle, stream, x, rms("rms_att", l), F32, c.eps,
+            w("wq", l, q * c.dim), w("wk", l, kv * c.dim), w("wv", l, kv * c.dim), BF16, c.dim,
+            c.n_heads, c.n_kv_heads, head, qb, *kv_ptr(l), BF16, c.max_seq, step, table),
+        "attention_partial": lambda l: call(
+            "ammon_attention_partial", rt.handle, stream, qb, c.n_heads, *kv_ptr(l), BF16,
+            c.n_kv_heads, head, c.max_seq, step, split, part),
+        "wo_residual": lambda l: call(
+            "ammon_gemv", rt.handle, stream, w("wo", l, c.dim * q), BF16, c.dim, q, xb, xr, xr),
+        "gate_up_swiglu": lambda l: call(
+            "ammon_gate_up_swiglu", rt.handle, stream, x, rms("rms_ffn", l), F32, c.eps,
+            w("w1", l, c.hidden * c.dim), w("w3", l, c.hidden * c.dim), BF16, c.dim, c.hidden,
+            hb),
+        "w2_residual": lambda l: call(
+            "ammon_gemv", rt.handle, stream, w("w2", l, c.dim * c.hidden), BF16, c.dim,
+            c.hidden, hb, xr, xr),
+        "lm_head": lambda l: call(
+            "ammon_gemv_rmsnorm", rt.handle, stream, x, weights["rms_final"], F32, c.eps,
+            weights["wcls"], BF16, c.vocab, c.dim, logits),
+    }
+    out = {}
+    nbytes = kernel_bytes(c, ctx)
+    for name, fn in launches.items():
+        timers = [Timer(rt) for _ in range(L)]
+        samples = []
+        for _ in range(reps):
+            for l in range(L):
+                timers[l].start(stream)
+                fn(l)
+                timers[l].stop(stream)
+            samples += [t.elapsed_ms() for t in timers]
+        for t in timers:
+            t.close()
+        ms = float(np.mean(samples))
+        out[name] = {"avg_us": round(ms * 1e3, 3), "bytes": nbytes[name],
+                     "gbs": round(nbytes[name] / (ms * 1e-3) / 1e9, 1),
+                     "frac": round(nbytes[name] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+                     "launches": len(samples)}
+    return out
+
+
+def cpu_baseline(rt, model, c, weights, start_pos, token0, gpu_tokens, budget_s):
+    """The oracle (C, OpenMP over output rows) decoding the same positions
+    from the same weights and KV prefix on the host cores."""
+    import oracle
+    from ammon_amd._abi import BF16, call
+
+    t0 = time.time()
+    host = {}
+    for name, buf in weights.items():
+        dt = np.float32 if name.startswith("rms") else np.uint16
+        host[name] = buf.download(buf.nbytes // np.dtype(dt).itemsize, dt)
+    shapes = oracle.weight_shapes(oracle.LlamaConfig(
+        **{k: LLAMA3_8B[k] for k in ("dim", "n_layers", "n_heads", "n_kv_heads", "hidden",
+                                     "vocab", "max_seq")}))
+    host = {k: v.reshape(shapes[k]) for k, v in host.items()}
+    ocfg = oracle.LlamaConfig(dim=c.dim, n_layers=c.n_layers, n_heads=c.n_heads,
+                              n_kv_heads=c.n_kv_heads, hidden=c.hidden, vocab=c.vocab,
+                              max_seq=c.max_seq, theta=c.theta, eps=c.eps, w_dtype=BF16,
+                              kv_dtype=BF16)
+    om = oracle.Model(ocfg, host)
+    head = c.dim // c.n_heads
+    kv_n = c.n_kv_heads * c.max_seq * head
+    for l in range(c.n_layers):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        call("ammon_llama_kv_layer", model.handle, l, ctypes.byref(k), ctypes.byref(v))
+        for src, get in ((k, oracle._lib.orc_model_key_cache),
+                         (v, oracle._lib.orc_model_value_cache)):
+            hm = np.empty(kv_n, np.uint16)
+            call("ammon_memcpy", rt.handle, hm.ctypes.data, src, hm.nbytes, 2, None)
+            rt.synchronize()
+            pm = oracle_layout(hm, c.n_kv_heads, c.max_seq, head)
+            ctypes.memmove(get(om._handle, l), pm.ctypes.data, pm.nbytes)
+    setup_s = time.time() - t0
+    log(f"cpu baseline: weights + cache on host in {setup_s:.1f}s; decoding")
+    tokens, times = [], []
+    tok = token0
+    pos = start_pos
+    while pos < c.max_seq:
+        t1 = time.perf_counter()
+        logits = om.step(tok, pos)
+        times.append(time.perf_counter() - t1)
+        tok = oracle.sample_argmax(logits)
+        tokens.append(tok)
+        pos += 1
+        if sum(times) > budget_s:
+            break
+    om.close()
+    n = len(times)
+    agree = [int(a) == int(b) for a, b in zip(tokens, gpu_tokens[:n])]
+    return {
+        "value": round(n / sum(times), 4), "unit": "tokens/s", "cores": oracle.num_threads(),
+        "kind": "port",
+        "sample": (f"{n} greedy decode tokens of the same model at positions {start_pos}.."
+                   f"{start_pos + n - 1} (ctx ~8192), oracle C restatement, -O3, OpenMP over "
+                   f"output rows"),
+        "seconds": round(sum(times), 2),
+        "token_parity": bool(all(agree)), "tokens_compared": n,
+    }
+
+
+def oracle_layout(head_major, kv_heads, seq, head):
+    from ammon_amd import kv_unpermute
+    return kv_unpermute(head_major.reshape(kv_heads, seq, head), kv_heads, seq, head)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=128)
+    ap.add_argument("--warmup", type=int, default=16)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--kernel-reps", type=int, default=3)
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
+                    help="seconds of CPU decode for the baseline (0 skips it)")
+    ap.add_argument("--no-graph", action="store_true", help="replay launches without a graph")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path "
+              f"is single-device. See DESIGN.md for how it would shard.", file=sys.stderr)
+        sys.exit(2)
+
+    import ammon_amd
+    from ammon_amd import Runtime, Timer
+    from ammon_amd._abi import BF16, call
+
+    c = Cfg(**LLAMA3_8B, w_dtype=BF16, kv_dtype=BF16)
+    total = args.steps + args.warmup
+    if total >= c.max_seq:
+        sys.exit("steps + warmup must be below the context length")
+    start_pos = c.max_seq - total
+    rt = Runtime(0)
+    log(f"device {rt.info.arch.decode()} cus={rt.info.compute_units}; generating weights")
+    t0 = time.time()
+    model = ammon_amd.LlamaModel.synthetic(rt, c, seed=2024, std=0.02,
+                                           use_graph=not args.no_graph)
+    head = c.dim // c.n_heads
+    kv_n = c.n_kv_heads * c.max_seq * head
+    for l in range(c.n_layers):
+        k, v = ctypes.c_void_p(), ctypes.c_void_p()
+        call("ammon_llama_kv_layer", model.handle, l, ctypes.byref(k), ctypes.byref(v))
+        rt.fill_normal(k, BF16, kv_n, 7, 2 * l)
+        rt.fill_normal(v, BF16, kv_n, 7, 2 * l + 1)
+    rt.synchronize()
+    log(f"weights + KV prefill in {time.time() - t0:.1f}s; launches/token={model.launches + 2}")
+
+    token0 = 128000
+    stream = model.stream
+    # Warmup continues the same greedy chain the timed steps extend; the
+    # first decode captures the token graph.
+    model.decode(token0, start_pos, args.warmup)
+    warm = model.read_tokens(start_pos, args.warmup)
+    next_token = int(warm[-1]) if args.warmup else token0
+    timer = Timer(rt)
+    t_wall = time.perf_counter()
+    timer.start(stream)
+    model.decode(next_token, start_pos + args.warmup, args.steps)
+    timer.stop(stream)
+    ms = timer.elapsed_ms()
+    wall = time.perf_counter() - t_wall
+    timer.close()
+    gpu_tokens = model.read_tokens(start_pos, total)
+    ms_per_step = ms / args.steps
+    tps = 1000.0 / ms_per_step
+    ctx_mid = start_pos + args.warmup + args.steps // 2
+    tok_bytes = token_bytes(c, ctx_mid)
+    log(f"{args.steps} tokens in {ms:.2f} ms (wall {wall * 1e3:.1f} ms): {tps:.1f} tok/s, "
+        f"{tok_bytes / (ms_per_step * 1e-3) / 1e9:.0f} GB/s per token stream")
+
+    kernels = time_kernels(rt, model, c, model.weights, ctx_mid, args.kernel_reps)
+    for k, v in kernels.items():
+        log(f"  {k:18s} {v['avg_us']:9.2f} us  {v['gbs']:7.1f} GB/s  frac {v['frac']:.3f}")
+    dom = kernels["gate_up_swiglu"]
+
+    cpu = None
+    if args.cpu_budget > 0 and not args.no_cpu:
+        cpu = cpu_baseline(rt, model, c, model.weights, start_pos, token0, gpu_tokens,
+                           args.cpu_budget)
+        log(f"cpu baseline: {cpu}")
+
+    result = {
+        "metric": METRIC,
+        "value": round(tps, 3),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("Llama-3-8B-shaped greedy decode at context 8192: 32 layers, dim 4096, "
+                         "32 q / 8 kv heads of 128, SwiGLU 14336, vocab 128256, RoPE theta "
+                         "500000; bf16 weights and KV cache, fp32 activations and "
+                         "accumulation; random N(0, 0.02) weights, KV prefilled N(0, 1)"),
+            "batch": 1,
+            "positions": [start_pos + args.warmup, c.max_seq - 1],
+            "graph_replay": not args.no_graph,
+            "launches_per_token": model.launches + 2,
+            "token_bytes": tok_bytes,
+            "token_hbm_gbs": round(tok_bytes / (ms_per_step * 1e-3) / 1e9, 1),
+            "token_roofline_frac": round(tok_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,
+                                         4),
+        },
+        "roofline": {
+            "kernel": "ammon_gemv_bf16_v_swiglu (gate/up GEMV + SwiGLU, RMSNorm prologue)",
+            "bound": "hbm",
+            "achieved": dom["gbs"],
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": dom["frac"],
+            "traffic": None,
+            "bytes_per_launch": dom["bytes"],
+            "avg_launch_us": dom["avg_us"],
+        },
+        "kernels": kernels,
+        "cpu_baseline": cpu,
+    }
+    model.close()
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

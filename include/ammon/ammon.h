@@ -118,6 +118,18 @@ ammon_status ammon_event_synchronize(ammon_runtime *rt, ammon_event ev);
 ammon_status ammon_event_elapsed_ms(ammon_runtime *rt, ammon_event start, ammon_event stop,
                                     float *ms);
 
+/* Launch-list replay.  A caller that records a sequence of the kernel calls
+ * below (the reference's Scheme record, src/blocks.rs:178-278) captures it
+ * once -- begin, make the calls on `stream`, end -- and replays the
+ * instantiated graph per token (the reference's Scheme::submit replay).
+ * Kernels read the token/position from a device ammon_decode_step, so the
+ * graph never changes between tokens. */
+typedef void *ammon_graph;
+ammon_status ammon_capture_begin(ammon_runtime *rt, ammon_stream stream);
+ammon_status ammon_capture_end(ammon_runtime *rt, ammon_stream stream, ammon_graph *out);
+ammon_status ammon_graph_launch(ammon_runtime *rt, ammon_graph graph, ammon_stream stream);
+ammon_status ammon_graph_destroy(ammon_runtime *rt, ammon_graph graph);
+
 /* Fill `count` elements with `value` (a kernel, not hipMemset, so it can be
  * captured in a graph). */
 ammon_status ammon_fill(ammon_runtime *rt, ammon_stream stream, void *dst, ammon_dtype dtype,
@@ -230,6 +242,12 @@ ammon_status ammon_add(ammon_runtime *rt, ammon_stream stream, const float *a, c
 ammon_status ammon_gemv(ammon_runtime *rt, ammon_stream stream, const void *w,
                         ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x, float *y,
                         const float *residual);
+/* The reference's position-strided gemv (src/kernels.rs:49-73; a test-only
+ * serial definition there): xout[step->position, :] = W x with xout
+ * [seq, d]. */
+ammon_status ammon_gemv_at_position(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                    ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                    float *xout, uint32_t seq, const ammon_decode_step *step);
 ammon_status ammon_gemv_rmsnorm(ammon_runtime *rt, ammon_stream stream, const float *x,
                                 const void *norm_weight, ammon_dtype norm_dtype, float eps,
                                 const void *w, ammon_dtype w_dtype, uint32_t d, uint32_t n,

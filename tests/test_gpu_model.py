@@ -1,0 +1,154 @@
+"""End-to-end GPU tests of the C++ host layer's model (modules + launch
+sequence + greedy loop) against the oracle: greedy token sequences identical;
+logits and KV caches within 1e-5 relative (normwise) with an fp32 KV cache
+(fp32 or identical bf16 weights); within 2e-2 -- the bf16 bar -- with a bf16
+KV cache, where a last-bit difference in the fp32 K/V before the store can
+flip one bf16 rounding (2^-8 relative); and within 2e-2 of the unrounded
+fp32 model for bf16 weights."""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import oracle
+from ammon_amd import AmmonError, LlamaModel
+from ammon_amd._abi import BF16, F32
+
+pytestmark = pytest.mark.gpu
+HERE = os.path.dirname(os.path.abspath(__file__))
+RTOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def tol(kv_dtype):
+    return RTOL if kv_dtype == F32 else BF16_TOL
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+@pytest.fixture(scope="module")
+def c1():
+    f = np.load(os.path.join(HERE, "golden", "c1_greedy.npz"))
+    cfg = oracle.LlamaConfig(**json.loads(str(f["config"])))
+    weights = oracle.random_weights(cfg, seed=int(f["weight_seed"]), std=0.02)
+    return cfg, weights, f
+
+
+def test_c1_greedy_tokens_match_fixture(rt, c1):
+    cfg, weights, f = c1
+    m = LlamaModel.from_host(rt, cfg, weights)
+    toks, logits, tps = m.generate_tokens(f["prompt"], int(f["max_new_tokens"]))
+    np.testing.assert_array_equal(toks, f["tokens"])
+    assert rel_err(logits, f["logits"]) <= RTOL
+    assert tps > 0
+    m.close()
+
+
+def test_c1_device_greedy_matches_fixture(rt, c1):
+    cfg, weights, f = c1
+    m = LlamaModel.from_host(rt, cfg, weights)
+    toks, logits, tps = m.generate_tokens_device(f["prompt"], int(f["max_new_tokens"]))
+    np.testing.assert_array_equal(toks, f["tokens"])
+    assert rel_err(logits, f["logits"]) <= RTOL
+    assert tps > 0
+    m.close()
+
+
+def test_c1_kv_cache_matches_oracle(rt, c1):
+    cfg, weights, f = c1
+    m = LlamaModel.from_host(rt, cfg, weights)
+    m.generate_tokens_device(f["prompt"], int(f["max_new_tokens"]))
+    om = oracle.Model(cfg, dict(weights))
+    om.generate_tokens(f["prompt"], int(f["max_new_tokens"]))
+    for layer in range(cfg.n_layers):
+        k, v = m.kv_layer(layer)
+        ok, ov = om.kv_layer(layer)
+        assert rel_err(k, ok) <= RTOL, layer
+        assert rel_err(v, ov) <= RTOL, layer
+    m.close()
+
+
+def test_graph_replay_equals_eager_launches(rt, c1):
+    cfg, weights, f = c1
+    dev = {k: rt.upload(np.ascontiguousarray(v)) for k, v in weights.items()}
+    graph = LlamaModel(rt, cfg, dev, use_graph=True)
+    eager = LlamaModel(rt, cfg, dev, use_graph=False)
+    for pos, tok in enumerate(f["prompt"][:5]):
+        np.testing.assert_array_equal(graph.step(int(tok), pos), eager.step(int(tok), pos))
+    graph.close()
+    eager.close()
+
+
+@pytest.mark.parametrize("stop_index", [3, 12])
+def test_stop_on_truncates_like_the_reference(rt, c1, stop_index):
+    cfg, weights, f = c1
+    stop = int(f["tokens"][stop_index])
+    want = list(f["tokens"][: list(f["tokens"]).index(stop)])
+    m = LlamaModel.from_host(rt, cfg, weights)
+    assert list(m.generate_tokens(f["prompt"], 256, stop_on=stop)[0]) == want
+    assert list(m.generate_tokens_device(f["prompt"], 256, stop_on=stop)[0]) == want
+    m.close()
+
+
+GQA = dict(dim=256, n_layers=3, n_heads=8, n_kv_heads=2, hidden=704, vocab=4099, max_seq=96,
+           theta=500000.0)
+
+
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+def test_gqa_bf16_weights_match_oracle(rt, kv_dtype):
+    cfg = oracle.LlamaConfig(**GQA, w_dtype=BF16, kv_dtype=kv_dtype)
+    weights = oracle.random_weights(cfg, seed=77, std=0.1)
+    prompt = [5, 4000, 17, 2048, 3]
+    m = LlamaModel.from_host(rt, cfg, weights)
+    toks, logits, _ = m.generate_tokens_device(prompt, cfg.max_seq)
+    want_toks, want_logits = oracle.Model(cfg, dict(weights)).generate_tokens(prompt, cfg.max_seq)
+    np.testing.assert_array_equal(toks, want_toks)
+    assert rel_err(logits, want_logits) <= tol(kv_dtype)
+    # bf16 weights against the unrounded fp32 model: per-step logits
+    cfg32 = oracle.LlamaConfig(**GQA, w_dtype=F32, kv_dtype=F32)
+    w32 = oracle.random_weights(cfg32, seed=77, std=0.1)
+    m32 = oracle.Model(cfg32, w32)
+    m.close()
+    m = LlamaModel.from_host(rt, cfg, weights)
+    for pos, tok in enumerate(prompt):
+        assert rel_err(m.step(tok, pos), m32.step(tok, pos)) <= 2e-2
+    m.close()
+
+
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+def test_llama3_8b_width_two_layers(rt, kv_dtype):
+    # Full Llama-3-8B layer width and vocab, two layers, bf16 weights.
+    cfg = oracle.LlamaConfig(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, hidden=14336,
+                             vocab=128256, max_seq=64, theta=500000.0, w_dtype=BF16,
+                             kv_dtype=kv_dtype)
+    weights = oracle.random_weights(cfg, seed=4, std=0.02)
+    prompt = [128000, 9906, 1917, 374]
+    m = LlamaModel.from_host(rt, cfg, weights)
+    toks, logits, _ = m.generate_tokens_device(prompt, 9)
+    want_toks, want_logits = oracle.Model(cfg, dict(weights)).generate_tokens(prompt, 9)
+    np.testing.assert_array_equal(toks, want_toks)
+    assert rel_err(logits, want_logits) <= tol(kv_dtype)
+    assert m.launches == 1 + 6 * cfg.n_layers + 1
+    m.close()
+
+
+def test_model_validation(rt, c1):
+    cfg, weights, f = c1
+    m = LlamaModel.from_host(rt, cfg, weights)
+    with pytest.raises(AmmonError, match="vocab"):
+        m.step(cfg.vocab, 0)
+    with pytest.raises(AmmonError, match="max_seq"):
+        m.step(1, cfg.max_seq)
+    with pytest.raises(AmmonError, match="max_seq"):
+        m.decode(1, cfg.max_seq - 2, 5)
+    with pytest.raises(AmmonError, match="prompt"):
+        m.generate_tokens([], 5)
+    m.close()
+    bad = oracle.LlamaConfig(**dict(json.loads(str(f["config"])), n_heads=7))
+    with pytest.raises(AmmonError, match="divisible"):
+        LlamaModel(rt, bad, m.weights)
