@@ -16,169 +16,271 @@
 //
 // Pass 2, one workgroup per q head: M = max m_s over live splits,
 // out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
+//
+// The reference uses fixed 8-position splits (src/kernels.rs:228-229); here
+// the split length is a launch parameter chosen to fill the device.
 #include "device_common.h"
 
-#define ATT_SMAX 1024      // positions per split
+#define ATT_ROUNDS 4         // position rounds per chunk held in registers
+#define ATT_CHUNK_MAX (ATT_ROUNDS * AMMON_WAVES * 32)  // positions per chunk, P2 >= 2
 #define ATT_MAX_SPLITS 4096
 #define ATT_MAX_HEAD 128
 
-template <typename KV, int CH, int GMAX>
+// Sum over aligned groups of `width` lanes (a power of two <= 64): DPP
+// inside 16-lane rows, shuffles across rows.
+AMMON_DEV float group_sum(float v, uint32_t width) {
+  v = group_sum16(v, width < 16 ? width : 16);
+  for (uint32_t off = 16; off < width; off <<= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+// One workgroup = one (split, kv head).  The split's positions are processed
+// in chunks of ATT_ROUNDS rounds; a round is 4 waves x (64 / P2) positions,
+// P2 lanes per position (the power of two >= head / CH).  Chunks are
+// double-buffered in registers: the next chunk's K and V loads are in flight
+// while the current one is processed.  For a chunk, the raw q.k dots go to
+// LDS, each wave turns one query head's dots into scores (the reference's
+// division by sqrt(head)), max and exp-sum, and the V chunk is accumulated
+// with the probabilities.  Chunks merge online (running max and sum per
+// head, uniform across the workgroup), so a split of any length is one pass;
+// with a single chunk the merge scales by exactly 1.  The per-lane V sums
+// are reduced across position slots and waves in LDS.
+// HEAD > 0 fixes the head width at compile time (then the lane layout and
+// the DPP reduction steps are constants); EXACT_G means q_heads / kv_heads
+// equals GMAX.  The generic instantiations (HEAD 0) read both at run time.
+template <int W> AMMON_DEV float group_sum_c(float v) {
+  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "power of two");
+  v += dpp_get<AMMON_DPP_XOR1>(v);
+  if (W >= 4) v += dpp_get<AMMON_DPP_XOR2>(v);
+  if (W >= 8) v += dpp_get<AMMON_DPP_HALF_MIRROR>(v);
+  if (W >= 16) v += dpp_get<AMMON_DPP_MIRROR>(v);
+  if (W >= 32) v += __shfl_xor(v, 16, 64);
+  if (W >= 64) v += __shfl_xor(v, 32, 64);
+  return v;
+}
+
+constexpr uint32_t ceil_pow2(uint32_t v) {
+  uint32_t p = 2;
+  while (p < v) p <<= 1;
+  return p;
+}
+
+template <typename KV, int CH, int GMAX, int HEAD, bool EXACT_G>
 AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
-  constexpr int U = 4;  // position rounds with loads in flight per lane
-  __shared__ float s_p[GMAX][ATT_SMAX];
-  __shared__ float s_red[AMMON_WAVES][GMAX * ATT_MAX_HEAD];
+  constexpr int R = ATT_ROUNDS;
+  // Probabilities of the current chunk, and after the last chunk the
+  // cross-slot reduction area (one padded row of GMAX * CH floats per lane).
+  constexpr int P_FLOATS = GMAX * ATT_CHUNK_MAX;
+  constexpr int RED_FLOATS = AMMON_WG * (GMAX * CH + 1);
+  __shared__ float s_lds[P_FLOATS > RED_FLOATS ? P_FLOATS : RED_FLOATS];
   __shared__ float s_ml[2][GMAX];
+  float(*s_p)[ATT_CHUNK_MAX] = (float(*)[ATT_CHUNK_MAX])s_lds;
+  float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])s_lds;
 
   const uint32_t split = blockIdx.x, g = blockIdx.y;
   const uint32_t pos = p.step->position;
   if (pos >= p.seq) return;
   const uint32_t t0 = split * p.split_len;
-  if (t0 > pos) return;  // dead split
+  if (t0 > pos) return;  // dead split: writes nothing
   const uint32_t n = min(p.split_len, pos + 1 - t0);
-  const uint32_t G = p.q_heads / p.kv_heads;
-  const uint32_t head = p.head;
+  const uint32_t G = EXACT_G ? (uint32_t)GMAX : p.q_heads / p.kv_heads;
+  const uint32_t head = HEAD > 0 ? (uint32_t)HEAD : p.head;
   const uint32_t LP = head / CH;
-  uint32_t P2 = 1;
-  while (P2 < LP) P2 <<= 1;
-  const uint32_t PW = 64 / P2;
+  uint32_t lg_p2 = 1;
+  while ((1u << lg_p2) < LP) ++lg_p2;
+  constexpr uint32_t P2C = HEAD > 0 ? ceil_pow2(HEAD / CH) : 0;
+  const uint32_t P2 = HEAD > 0 ? P2C : (1u << lg_p2);
+  if (HEAD > 0) lg_p2 = __builtin_ctz(P2C > 0 ? P2C : 2);
+  const uint32_t lg_pw = 6 - lg_p2;
+  const uint32_t PW = 1u << lg_pw;
   const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const uint32_t sub = lane & (P2 - 1), slot = lane / P2;
   const bool active = sub < LP;
   const uint32_t round = AMMON_WAVES * PW;
+  const uint32_t chunk = R * round;  // <= ATT_CHUNK_MAX since P2 >= 2
+  using C = Chunk<KV, CH>;
+  using QC = Chunk<float, (CH >= 4 ? 4 : CH)>;
+  constexpr int QCH = CH >= 4 ? 4 : CH;
 
   float qr[GMAX][CH];
 #pragma unroll
-  for (int j = 0; j < GMAX; ++j)
+  for (int j = 0; j < GMAX; ++j) {
+    const bool ok = (uint32_t)j < G && active;
+    const float *qp = p.q + (size_t)(g * G + (ok ? j : 0)) * head + sub * CH;
 #pragma unroll
-    for (int c = 0; c < CH; ++c)
-      qr[j][c] = ((uint32_t)j < G && active)
-                     ? p.q[(size_t)(g * G + j) * head + sub * CH + c]
-                     : 0.f;
+    for (int c = 0; c < CH; c += QCH) {
+      float f[QCH];
+      QC::widen(ok ? QC::load(qp + c) : QC::zero(), f);
+#pragma unroll
+      for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
+    }
+  }
 
-  const KV *kb = (const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head + sub * CH;
-  const KV *vb = (const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head + sub * CH;
+  // Buffer resources over this split's valid positions: inactive lanes and
+  // positions past the chunk read zero through an out-of-range offset.
+  const uint32_t es = (uint32_t)sizeof(KV);
+  const __amdgpu_buffer_rsrc_t kres =
+      make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
+  const __amdgpu_buffer_rsrc_t vres =
+      make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
   const float root = sqrtf((float)head);
-  using C = Chunk<KV, CH>;
 
-  // Scores.
-  for (uint32_t base = 0; base < n; base += round * U) {
-    typename C::V raw[U];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tl = base + u * round + wave * PW + slot;
-      raw[u] = (tl < n && active) ? C::load(kb + (size_t)tl * head) : C::zero();
-    }
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tl = base + u * round + wave * PW + slot;
-      float kf[CH];
-      C::widen(raw[u], kf);
-      float d[GMAX];
-#pragma unroll
-      for (int j = 0; j < GMAX; ++j) {
-        float s = 0.f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) s += qr[j][c] * kf[c];
-        d[j] = s;
-      }
-      for (uint32_t off = P2 >> 1; off > 0; off >>= 1)
-#pragma unroll
-        for (int j = 0; j < GMAX; ++j) d[j] += __shfl_xor(d[j], off, 64);
-      if (sub == 0 && tl < n)
-#pragma unroll
-        for (int j = 0; j < GMAX; ++j)
-          if ((uint32_t)j < G) s_p[j][tl] = d[j] / root;
-    }
-  }
-  __syncthreads();
-
-  // Split max and exp-sum per query head.
-  for (uint32_t j = wave; j < G; j += AMMON_WAVES) {
-    float m = -INFINITY;
-    for (uint32_t t = lane; t < n; t += 64) m = fmaxf(m, s_p[j][t]);
-    m = wave_max(m);
-    float l = 0.f;
-    for (uint32_t t = lane; t < n; t += 64) {
-      const float e = expf(s_p[j][t] - m);
-      s_p[j][t] = e;
-      l += e;
-    }
-    l = wave_sum(l);
-    if (lane == 0) {
-      s_ml[0][j] = m;
-      s_ml[1][j] = l;
-    }
-  }
-  __syncthreads();
-
-  // Probability-weighted V.
   float acc[GMAX][CH];
+  float m_run[GMAX], l_run[GMAX];
 #pragma unroll
-  for (int j = 0; j < GMAX; ++j)
+  for (int j = 0; j < GMAX; ++j) {
+    m_run[j] = -INFINITY;
+    l_run[j] = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) acc[j][c] = 0.f;
-  for (uint32_t base = 0; base < n; base += round * U) {
-    typename C::V raw[U];
+  }
+
+  // Chunk pipeline: two register buffers of K and V; while one chunk is
+  // scored and accumulated the next one's loads are in flight.
+  using VT = typename C::V;
+  auto load_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
+    const uint32_t cn = c0 < n ? min(chunk, n - c0) : 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tl = base + u * round + wave * PW + slot;
-      raw[u] = (tl < n && active) ? C::load(vb + (size_t)tl * head) : C::zero();
+    for (int r = 0; r < R; ++r) {
+      const uint32_t tl = r * round + wave * PW + slot;
+      const uint32_t off = (tl < cn && active) ? ((c0 + tl) * head + sub * CH) * es : AMMON_OOB;
+      kr[r] = C::load_buf(kres, off);
+      vr[r] = C::load_buf(vres, off);
+    }
+  };
+  auto compute_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
+    const uint32_t cn = min(chunk, n - c0);
+    if (c0 > 0) __syncthreads();  // previous chunk's probabilities consumed
+
+    // raw q.k dots: this lane's CH dims, then the P2 lanes of the position
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t tl = r * round + wave * PW + slot;
+      float kf[CH];
+      C::widen(kr[r], kf);
+#pragma unroll
+      for (int j = 0; j < GMAX; ++j) {
+        float sacc = 0.f;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) sacc += qr[j][c] * kf[c];
+        if constexpr (HEAD > 0)
+          sacc = group_sum_c<P2C>(sacc);
+        else
+          sacc = group_sum(sacc, P2);
+        if (sub == 0 && tl < cn && (uint32_t)j < G) s_p[j][tl] = sacc;
+      }
+    }
+    __syncthreads();
+
+    // scores = dot / sqrt(head) (reference src/kernels.rs:298), chunk max
+    // and exp-sum per query head (one wave per head)
+    for (uint32_t j = wave; j < G; j += AMMON_WAVES) {
+      float m = -INFINITY;
+      for (uint32_t t = lane; t < cn; t += 64) {
+        const float sc = s_p[j][t] / root;
+        s_p[j][t] = sc;
+        m = fmaxf(m, sc);
+      }
+      m = wave_max(m);
+      float l = 0.f;
+      for (uint32_t t = lane; t < cn; t += 64) {
+        const float e = expf(s_p[j][t] - m);
+        s_p[j][t] = e;
+        l += e;
+      }
+      l = wave_sum(l);
+      if (lane == 0) {
+        s_ml[0][j] = m;
+        s_ml[1][j] = l;
+      }
+    }
+    __syncthreads();
+
+    // online merge with the previous chunks, then accumulate V
+    float scale[GMAX];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      scale[j] = 0.f;
+      if ((uint32_t)j < G) {
+        const float cm = s_ml[0][j], cl = s_ml[1][j];
+        const float M = fmaxf(m_run[j], cm);
+        const float a = expf(m_run[j] - M), b = expf(cm - M);
+        if (c0 > 0)
+#pragma unroll
+          for (int c = 0; c < CH; ++c) acc[j][c] *= a;
+        l_run[j] = l_run[j] * a + cl * b;
+        m_run[j] = M;
+        scale[j] = b;
+      }
     }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t tl = base + u * round + wave * PW + slot;
-      if (tl < n) {
+    for (int r = 0; r < R; ++r) {
+      const uint32_t tl = r * round + wave * PW + slot;
+      if (tl < cn) {
         float vf[CH];
-        C::widen(raw[u], vf);
+        C::widen(vr[r], vf);
 #pragma unroll
         for (int j = 0; j < GMAX; ++j) {
-          const float pj = ((uint32_t)j < G) ? s_p[j][tl] : 0.f;
+          const float pj = ((uint32_t)j < G) ? s_p[j][tl] * scale[j] : 0.f;
 #pragma unroll
           for (int c = 0; c < CH; ++c) acc[j][c] += pj * vf[c];
         }
       }
     }
-  }
-  for (uint32_t off = P2; off < 64; off <<= 1)
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j)
-#pragma unroll
-      for (int c = 0; c < CH; ++c) acc[j][c] += __shfl_xor(acc[j][c], off, 64);
-  if (slot == 0 && active)
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j)
-      if ((uint32_t)j < G)
-#pragma unroll
-        for (int c = 0; c < CH; ++c) s_red[wave][j * head + sub * CH + c] = acc[j][c];
-  __syncthreads();
+  };
 
-  const uint32_t slot_w = head + 2;
-  for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
-    const uint32_t j = idx / head, d = idx % head;
-    float total = s_red[0][idx];
+  VT kA[R], vA[R], kB[R], vB[R];
+  load_chunk(0, kA, vA);
+  load_chunk(chunk, kB, vB);
+  for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
+    compute_chunk(c0, kA, vA);
+    load_chunk(c0 + 2 * chunk, kA, vA);
+    if (c0 + chunk >= n) break;
+    compute_chunk(c0 + chunk, kB, vB);
+    load_chunk(c0 + 3 * chunk, kB, vB);
+  }
+
+  // reduce acc over the 4 * PW position slots of the workgroup through LDS
+  // (the probability area is reused: wait until every wave is done with it)
+  __syncthreads();
 #pragma unroll
-    for (int w = 1; w < AMMON_WAVES; ++w) total += s_red[w][idx];
+  for (int j = 0; j < GMAX; ++j)
+#pragma unroll
+    for (int c = 0; c < CH; ++c) s_red[threadIdx.x][j * CH + c] = acc[j][c];
+  __syncthreads();
+  const uint32_t slot_w = head + 2;
+  const uint32_t slots = AMMON_WAVES * PW;
+  for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
+    const uint32_t j = idx / head, d = idx - j * head;
+    const uint32_t sb = d / CH, c = d % CH;  // lane sub and element (CH is a constant)
+    float total = 0.f;
+    for (uint32_t s = 0; s < slots; ++s) {
+      // thread of (wave s / PW, slot s % PW, sub sb)
+      const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
+      total += s_red[t][j * CH + c];
+    }
     p.partial[((size_t)(g * G + j) * p.splits + split) * slot_w + d] = total;
   }
   if (threadIdx.x < G) {
     const uint32_t j = threadIdx.x;
     float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
-    o[head] = s_ml[0][j];
-    o[head + 1] = s_ml[1][j];
+    o[head] = m_run[j];
+    o[head + 1] = l_run[j];
   }
 }
 
-#define ATT_PARTIAL(NAME, KV, CH, GMAX)                                          \
+#define ATT_PARTIAL(NAME, KV, CH, GMAX, HEAD, EXACT)                             \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
-    attention_partial_body<KV, CH, GMAX>(p);                                     \
+    attention_partial_body<KV, CH, GMAX, HEAD, EXACT>(p);                        \
   }
 
-#define ATT_PARTIAL_G(PREFIX, KV, CH)          \
-  ATT_PARTIAL(PREFIX##_g1, KV, CH, 1)          \
-  ATT_PARTIAL(PREFIX##_g2, KV, CH, 2)          \
-  ATT_PARTIAL(PREFIX##_g4, KV, CH, 4)          \
-  ATT_PARTIAL(PREFIX##_g8, KV, CH, 8)
+#define ATT_PARTIAL_G(PREFIX, KV, CH)                  \
+  ATT_PARTIAL(PREFIX##_g1, KV, CH, 1, 0, false)        \
+  ATT_PARTIAL(PREFIX##_g2, KV, CH, 2, 0, false)        \
+  ATT_PARTIAL(PREFIX##_g4, KV, CH, 4, 0, false)        \
+  ATT_PARTIAL(PREFIX##_g8, KV, CH, 8, 0, false)
 
+// generic: any head <= 128 and group size <= 8
 ATT_PARTIAL_G(ammon_attention_partial_f32_c4, float, 4)
 ATT_PARTIAL_G(ammon_attention_partial_f32_c2, float, 2)
 ATT_PARTIAL_G(ammon_attention_partial_f32_c1, float, 1)
@@ -187,41 +289,69 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c4, uint16_t, 4)
 ATT_PARTIAL_G(ammon_attention_partial_bf16_c2, uint16_t, 2)
 ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 
+// head 128 with a power-of-two group (Llama-3 shapes): compile-time layout
+#define ATT_PARTIAL_H128(PREFIX, KV, CH)               \
+  ATT_PARTIAL(PREFIX##_g1, KV, CH, 1, 128, true)       \
+  ATT_PARTIAL(PREFIX##_g2, KV, CH, 2, 128, true)       \
+  ATT_PARTIAL(PREFIX##_g4, KV, CH, 4, 128, true)       \
+  ATT_PARTIAL(PREFIX##_g8, KV, CH, 8, 128, true)
+
+ATT_PARTIAL_H128(ammon_attention_partial_h128_bf16_c8, uint16_t, 8)
+ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
+
+// Pass 2: grid (q heads, head / 32 dim slices).  Every lane first loads, for
+// one live split, that split's max, sum and 8 of the slice's dims (one
+// round trip); the workgroup max M gives each split's weight e^{m_s - M};
+// the weighted dims and sums are reduced over the splits in LDS.  Splits
+// beyond 64 per pass are folded in by further passes over the same buffers.
+// Every workgroup of a head computes the same M and L.
+#define COMB_SPLIT_LANES 64
 extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine(ammon_k_attention p) {
-  __shared__ float s_w[ATT_MAX_SPLITS];
-  __shared__ float s_acc[AMMON_WG];
+  __shared__ float s_acc[COMB_SPLIT_LANES][33];
+  __shared__ float s_l[COMB_SPLIT_LANES];
   __shared__ float red[AMMON_WAVES];
-  const uint32_t h = blockIdx.x;
+  const uint32_t h = blockIdx.x, slice = blockIdx.y;
   const uint32_t head = p.head, slot = head + 2;
+  const uint32_t d0 = slice * 32;
   float *out = p.out + (size_t)h * head;
   const uint32_t pos = p.step->position;
   if (pos >= p.seq) {
-    for (uint32_t d = threadIdx.x; d < head; d += AMMON_WG) out[d] = __uint_as_float(0x7fc00000u);
+    if (threadIdx.x < 32 && d0 + threadIdx.x < head) out[d0 + threadIdx.x] = __uint_as_float(0x7fc00000u);
     return;
   }
   const uint32_t live = pos / p.split_len + 1;
   const float *base = p.partial + (size_t)h * p.splits * slot;
+  const uint32_t sl = threadIdx.x >> 2;        // split lane, 0..63
+  const uint32_t dq = (threadIdx.x & 3) * 8;   // 8 dims of the slice
 
+  // M over all live splits
   float m = -INFINITY;
   for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) m = fmaxf(m, base[(size_t)s * slot + head]);
   const float M = block_max(m, red);
-  for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG)
-    s_w[s] = expf(base[(size_t)s * slot + head] - M);
-  __syncthreads();
-  float l = 0.f;
-  for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) l += base[(size_t)s * slot + head + 1] * s_w[s];
-  const float L = block_sum(l, red);
 
-  const uint32_t ways = AMMON_WG / head;
-  const uint32_t way = threadIdx.x / head, d = threadIdx.x % head;
-  float acc = 0.f;
-  if (way < ways)
-    for (uint32_t s = way; s < live; s += ways) acc += base[(size_t)s * slot + d] * s_w[s];
-  s_acc[threadIdx.x] = acc;
+  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float l = 0.f;
+  for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
+    const float *row = base + (size_t)s * slot;
+    const float w = expf(row[head] - M);
+    if ((threadIdx.x & 3) == 0) l += row[head + 1] * w;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t d = d0 + dq + k;
+      if (d < head) a[k] += row[d] * w;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < 8; ++k) s_acc[sl][dq + k] = a[k];
+  if ((threadIdx.x & 3) == 0) s_l[sl] = l;
   __syncthreads();
-  if (threadIdx.x < head) {
-    float total = s_acc[threadIdx.x];
-    for (uint32_t w = 1; w < ways; ++w) total += s_acc[w * head + threadIdx.x];
-    out[threadIdx.x] = total / L;
+  if (threadIdx.x < 32) {
+    float total = 0.f, L = 0.f;
+    for (uint32_t s = 0; s < COMB_SPLIT_LANES; ++s) {
+      total += s_acc[s][threadIdx.x];
+      L += s_l[s];
+    }
+    const uint32_t d = d0 + threadIdx.x;
+    if (d < head) out[d] = total / L;
   }
 }

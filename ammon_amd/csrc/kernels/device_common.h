@@ -42,12 +42,25 @@ typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x2 __attribute__((ext_vector_type(2)));
 
+// Buffer resource (V#) over [base, base + bytes): raw buffer loads at byte
+// offsets >= bytes return zero and touch no memory, which replaces
+// per-lane bounds branches.  Dword 3 is the gfx9-family raw-buffer format.
+#define AMMON_BUFFER_DWORD3 0x00020000
+AMMON_DEV __amdgpu_buffer_rsrc_t make_rsrc(const void *base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)base, (short)0, (int)bytes, AMMON_BUFFER_DWORD3);
+}
+#define AMMON_OOB 0x80000000u  // a byte offset past every buffer used here
+
 // Chunk<T, CH>: CH consecutive elements of storage type T (float or bf16
 // stored as uint16_t) loaded with one vector load and widened to fp32.
+// load_buf reads the chunk at byte offset `off` of a buffer resource.
 template <typename T, int CH> struct Chunk;
 
 template <> struct Chunk<uint16_t, 8> {
   using V = u32x4;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  }
   static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0u, 0u, 0u, 0u}; }
@@ -61,6 +74,9 @@ template <> struct Chunk<uint16_t, 8> {
 
 template <> struct Chunk<uint16_t, 4> {
   using V = u32x2;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+  }
   static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0u, 0u}; }
@@ -72,6 +88,9 @@ template <> struct Chunk<uint16_t, 4> {
 
 template <> struct Chunk<uint16_t, 2> {
   using V = uint32_t;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
   static AMMON_DEV V load(const uint16_t *p) { return *(const uint32_t *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) {
     return __builtin_nontemporal_load((const uint32_t *)p);
@@ -82,6 +101,9 @@ template <> struct Chunk<uint16_t, 2> {
 
 template <> struct Chunk<uint16_t, 1> {
   using V = uint16_t;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+  }
   static AMMON_DEV V load(const uint16_t *p) { return *p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return *p; }
   static AMMON_DEV V zero() { return 0; }
@@ -90,6 +112,9 @@ template <> struct Chunk<uint16_t, 1> {
 
 template <> struct Chunk<float, 4> {
   using V = f32x4;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0.f, 0.f, 0.f, 0.f}; }
@@ -98,6 +123,9 @@ template <> struct Chunk<float, 4> {
 
 template <> struct Chunk<float, 2> {
   using V = f32x2;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+  }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0.f, 0.f}; }
@@ -106,6 +134,9 @@ template <> struct Chunk<float, 2> {
 
 template <> struct Chunk<float, 1> {
   using V = float;
+  static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+  }
   static AMMON_DEV V load(const float *p) { return *p; }
   static AMMON_DEV V load_nt(const float *p) { return *p; }
   static AMMON_DEV V zero() { return 0.f; }
@@ -113,17 +144,64 @@ template <> struct Chunk<float, 1> {
 };
 
 // ---- reductions --------------------------------------------------------------
-// Butterfly reductions: every participating lane ends with the identical
-// value, and the association order is fixed, so results are deterministic.
+// DPP reductions inside 16-lane rows.  Each step is one VALU op reading a
+// permuted neighbour: quad_perm [1,0,3,2] (xor 1), quad_perm [2,3,0,1]
+// (xor 2), row_half_mirror (pairs quads 0/1, 2/3) and row_mirror (pairs
+// half rows).  After the steps up to WIDTH every lane of a WIDTH-lane group
+// holds the group's total; both operands of each add hold identically
+// associated partial sums, so the lanes agree bit for bit.
+#define AMMON_DPP_XOR1 0xB1
+#define AMMON_DPP_XOR2 0x4E
+#define AMMON_DPP_HALF_MIRROR 0x141
+#define AMMON_DPP_MIRROR 0x140
+
+template <int CTRL> AMMON_DEV float dpp_get(float v) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), CTRL, 0xF, 0xF, false));
+}
+
+AMMON_DEV float lane_get(float v, int lane) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+// Whole-wave reductions (call with all 64 lanes active): the four DPP
+// steps give each 16-lane row its total, the row totals are read into
+// scalar registers and combined as (r0 + r1) + (r2 + r3).  Every lane gets
+// the identical, deterministically associated value.  Narrower widths use
+// an xor butterfly.
 template <int WIDTH = 64> AMMON_DEV float wave_sum(float v) {
+  if constexpr (WIDTH == 64) {
+    v += dpp_get<AMMON_DPP_XOR1>(v);
+    v += dpp_get<AMMON_DPP_XOR2>(v);
+    v += dpp_get<AMMON_DPP_HALF_MIRROR>(v);
+    v += dpp_get<AMMON_DPP_MIRROR>(v);
+    return (lane_get(v, 0) + lane_get(v, 16)) + (lane_get(v, 32) + lane_get(v, 48));
+  } else {
 #pragma unroll
-  for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-  return v;
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+  }
 }
 
 template <int WIDTH = 64> AMMON_DEV float wave_max(float v) {
+  if constexpr (WIDTH == 64) {
+    v = fmaxf(v, dpp_get<AMMON_DPP_XOR1>(v));
+    v = fmaxf(v, dpp_get<AMMON_DPP_XOR2>(v));
+    v = fmaxf(v, dpp_get<AMMON_DPP_HALF_MIRROR>(v));
+    v = fmaxf(v, dpp_get<AMMON_DPP_MIRROR>(v));
+    return fmaxf(fmaxf(lane_get(v, 0), lane_get(v, 16)), fmaxf(lane_get(v, 32), lane_get(v, 48)));
+  } else {
 #pragma unroll
-  for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    for (int off = WIDTH / 2; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+    return v;
+  }
+}
+
+// Sum over aligned groups of `width` lanes (width in {1, 2, 4, 8, 16}).
+AMMON_DEV float group_sum16(float v, uint32_t width) {
+  if (width >= 2) v += dpp_get<AMMON_DPP_XOR1>(v);
+  if (width >= 4) v += dpp_get<AMMON_DPP_XOR2>(v);
+  if (width >= 8) v += dpp_get<AMMON_DPP_HALF_MIRROR>(v);
+  if (width >= 16) v += dpp_get<AMMON_DPP_MIRROR>(v);
   return v;
 }
 

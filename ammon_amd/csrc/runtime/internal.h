@@ -5,7 +5,10 @@
 
 #include <cstdarg>
 #include <cstdint>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../kernel_params.h"
@@ -25,6 +28,8 @@ struct Kernels {
   hipFunction_t rope = nullptr;
   hipFunction_t cache_store = nullptr;
   hipFunction_t att_partial[2][kAttChunks][kAttGroups] = {};
+  // head-128 specialisations: [dtype][group index], widest chunk only
+  hipFunction_t att_partial_h128[2][kAttGroups] = {};
   hipFunction_t att_combine = nullptr;
   hipFunction_t gemv[2][2][kGemvModes] = {};
   hipFunction_t swiglu = nullptr;
@@ -40,8 +45,13 @@ constexpr uint32_t kLdsPerCu = 160 * 1024;
 
 // GEMV rows per wave and waves per workgroup (must match gemv.hip).
 constexpr uint32_t kGemvRowsPerWave = 2;
+constexpr uint32_t kGemvTileChunks = 4;  // U: chunks per lane per tile
 constexpr uint32_t kGemvWaves = 4;
 constexpr uint32_t kWorkgroup = 256;
+
+// Resident workgroups of `f` per CU at 256 threads and `shmem` bytes of
+// dynamic LDS (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor, cached).
+uint32_t occupancy(ammon_runtime *rt, hipFunction_t f, size_t shmem);
 
 ammon_status set_error(ammon_status st, const char *fmt, ...)
     __attribute__((format(printf, 2, 3)));
@@ -57,6 +67,8 @@ struct ammon_runtime {
   ammon_rt::Kernels k;
   ammon_device_info info = {};
   uint32_t gemv_wgs_per_cu = 4;
+  std::mutex occ_mu;
+  std::map<std::pair<hipFunction_t, size_t>, uint32_t> occ_cache;
 };
 
 #define AMMON_HIP(expr)                                            \

@@ -89,7 +89,14 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   AMMON_CHECK(a.n > 0 && a.d > 0, "%s: empty matrix (d=%u, n=%u)", what, a.d, a.n);
   AMMON_CHECK(!a.norm_w || valid_dtype(a.norm_dtype), "%s: unknown norm dtype", what);
   AMMON_CHECK(!a.norm_w || (std::isfinite(a.eps) && a.eps >= 0.f), "%s: eps must be finite and >= 0", what);
-  const size_t shmem = (size_t)a.n * sizeof(float);
+  // x staged in LDS, zero-padded to whole tiles of 64 lanes x kGemvTileChunks
+  // chunks of 16 bytes (8 bf16 or 4 fp32 weights; 1 weight on the scalar path).
+  const bool bf = a.w_dtype == AMMON_BF16;
+  const uint32_t ch_v = bf ? 8 : 4;
+  const uintptr_t wbits = (uintptr_t)a.w0 | (uintptr_t)a.w1 | (uintptr_t)a.w2;
+  const int vec_ok = (a.n % ch_v == 0) && (wbits & 15u) == 0;
+  const uint64_t tile_elems = 64ull * kGemvTileChunks * (vec_ok ? ch_v : 1);
+  const size_t shmem = (size_t)((a.n + tile_elems - 1) / tile_elems * tile_elems) * sizeof(float);
   AMMON_CHECK(shmem <= (size_t)rt->info.max_shared_per_block,
               "%s: reduction length n=%u needs %zu bytes of LDS; the device allows %d", what, a.n,
               shmem, rt->info.max_shared_per_block);
@@ -100,10 +107,6 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     AMMON_CHECK(!overlaps(a.x, (size_t)a.n * 4, a.residual, ybytes), "%s: residual overlaps x", what);
   if (stream == AMMON_STREAM_VALIDATE) return AMMON_OK;
 
-  const int dt = a.w_dtype == AMMON_BF16 ? 1 : 0;
-  const uint32_t ch = dt ? 8 : 4;
-  uintptr_t bits = (uintptr_t)a.w0 | (uintptr_t)a.w1 | (uintptr_t)a.w2;
-  const int vec = (a.n % ch == 0) && (bits & 15u) == 0;
 
   ammon_k_gemv p = {};
   p.w0 = a.w0;
@@ -129,11 +132,28 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   p.seq = a.seq;
   p.kv_dtype = (uint32_t)a.kv_dtype;
 
+  const int dt = bf ? 1 : 0;
+  const int vec = vec_ok;
+  // Grid: at most gemv_wgs_per_cu resident workgroups per CU (fewer if LDS
+  // bounds it); among 2..max per CU pick the count whose grid-stride split of
+  // the row blocks wastes the least (blocks / (grid * blocks per workgroup)).
   const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
-  const uint32_t lds_fit = std::max<uint32_t>(1, (uint32_t)(kLdsPerCu / (shmem + 64)));
-  const uint32_t per_cu = std::min(rt->gemv_wgs_per_cu, lds_fit);
-  const uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * per_cu);
-  return launch(rt, stream, rt->k.gemv[dt][vec][a.mode], grid, 1, (uint32_t)shmem, p, what);
+  hipFunction_t fn = rt->k.gemv[dt][vec][a.mode];
+  const uint32_t resident = occupancy(rt, fn, shmem);
+  const uint32_t max_per_cu = std::max<uint32_t>(1, std::min(rt->gemv_wgs_per_cu, resident));
+  uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * max_per_cu);
+  double best = -1.0;
+  for (uint32_t w = max_per_cu; w >= 1; --w) {
+    const uint32_t g = std::min<uint32_t>(p.row_blocks, cus * w);
+    const uint32_t per_wg = cdiv(p.row_blocks, g);
+    const double eff = (double)p.row_blocks / ((double)g * per_wg);
+    if (eff > best + 1e-9) {
+      best = eff;
+      grid = g;
+    }
+    if (w == 1 || w <= max_per_cu / 2) break;
+  }
+  return launch(rt, stream, fn, grid, 1, (uint32_t)shmem, p, what);
 }
 
 // ---- attention ------------------------------------------------------------------
@@ -301,8 +321,11 @@ ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, con
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, nullptr,
                          q_heads, kv_heads, head, seq, split_len, splits};
   const int dt = kv_dtype == AMMON_BF16 ? 1 : 0;
-  return launch(rt, stream, rt->k.att_partial[dt][ci][gi], splits, kv_heads, 0, p,
-                "attention_partial");
+  const uint32_t g = q_heads / kv_heads;
+  // head 128, widest chunk, power-of-two group: the compile-time variant
+  const bool h128 = head == 128 && ci == (dt ? 0 : 1) && (g & (g - 1)) == 0;
+  hipFunction_t f = h128 ? rt->k.att_partial_h128[dt][gi] : rt->k.att_partial[dt][ci][gi];
+  return launch(rt, stream, f, splits, kv_heads, 0, p, "attention_partial");
 }
 
 ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
@@ -325,7 +348,8 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
                          ammon_attention_splits(seq, split_len)};
-  return launch(rt, stream, rt->k.att_combine, q_heads, 1, 0, p, "attention_combine");
+  return launch(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), 0, p,
+                "attention_combine");
 }
 
 ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, const float *q,

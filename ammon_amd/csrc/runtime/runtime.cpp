@@ -49,6 +49,19 @@ ammon_status hip_error(hipError_t e, const char *what) {
   return set_error(AMMON_E_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+uint32_t occupancy(ammon_runtime *rt, hipFunction_t f, size_t shmem) {
+  std::lock_guard<std::mutex> lock(rt->occ_mu);
+  const auto key = std::make_pair(f, shmem);
+  auto it = rt->occ_cache.find(key);
+  if (it != rt->occ_cache.end()) return it->second;
+  int blocks = 0;
+  if (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&blocks, f, 256, shmem) != hipSuccess ||
+      blocks < 1)
+    blocks = 1;
+  rt->occ_cache[key] = (uint32_t)blocks;
+  return (uint32_t)blocks;
+}
+
 static std::mutex g_mu;
 static std::map<int, ammon_runtime *> g_runtimes;
 
@@ -92,6 +105,13 @@ static ammon_status load_kernels(ammon_runtime *rt) {
         snprintf(name, sizeof name, "ammon_attention_partial_%s_c%d_g%d", dtn[d], chs[c], gs[g]);
         R(3, name, k.att_partial[d][c][g]);
       }
+    }
+  for (int d = 0; d < 2; ++d)
+    for (int g = 0; g < kAttGroups; ++g) {
+      char name[96];
+      snprintf(name, sizeof name, "ammon_attention_partial_h128_%s_g%d",
+               d ? "bf16_c8" : "f32_c4", gs[g]);
+      R(3, name, k.att_partial_h128[d][g]);
     }
   const char *modes[kGemvModes] = {"plain", "residual", "swiglu", "qkv"};
   for (int d = 0; d < 2; ++d)
@@ -429,12 +449,14 @@ size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t s
   return (size_t)q_heads * ammon_attention_splits(seq, split_len) * (head + 2) * sizeof(float);
 }
 
-// Aim for about four workgroups per CU at full context; splits stay between
-// 16 and AMMON_ATTENTION_MAX_SPLIT positions and the count under
-// AMMON_ATTENTION_MAX_SPLITS.
+// Aim for about two workgroups per CU at full context: the partial kernel
+// pipelines two chunks of K and V (64 positions of a 128-wide bf16 head
+// each) through registers, so a workgroup overlaps its own loads and
+// arithmetic.  Splits stay between 16 and AMMON_ATTENTION_MAX_SPLIT
+// positions and the count under AMMON_ATTENTION_MAX_SPLITS.
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq) {
   const uint32_t cus = rt ? (uint32_t)rt->info.compute_units : 256u;
-  const uint64_t target_wgs = 4ull * (cus ? cus : 256u);
+  const uint64_t target_wgs = 2ull * (cus ? cus : 256u);
   uint32_t split = 16;
   while (split < AMMON_ATTENTION_MAX_SPLIT &&
          ((uint64_t)kv_heads * ammon_attention_splits(seq, split) > target_wgs ||

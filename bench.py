@@ -65,10 +65,10 @@ def kernel_bytes(c, ctx):
     }
 
 
-def time_kernels(rt, model, c, weights, ctx, reps):
-    """Average duration of each fused kernel, from HIP events around every
-    launch on the model's stream, cycling through all layers' weights so
-    nothing is served from cache."""
+def time_kernels(rt, model, c, weights, ctx, reps, split=0):
+    """Average duration of each fused kernel: HIP events on the model's
+    stream around batches of back-to-back launches that cycle through all
+    layers' weights, so nothing is served from cache."""
     import ammon_amd
     from ammon_amd import Timer
     from ammon_amd._abi import BF16, F32, call
@@ -83,7 +83,8 @@ def time_kernels(rt, model, c, weights, ctx, reps):
     logits = rt.alloc(c.vocab * 4)
     step = rt.step(1, ctx - 1)
     table = rt.upload(ammon_amd.rope_table_host(c.theta, head, c.max_seq))
-    split = int(ammon_amd._abi.lib.ammon_attention_default_split(rt.handle, kv, c.max_seq))
+    if not split:
+        split = int(ammon_amd._abi.lib.ammon_attention_default_split(rt.handle, c.n_kv_heads, c.max_seq))
     part = rt.alloc(ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split))
     rt.synchronize()
 
@@ -119,22 +120,24 @@ def time_kernels(rt, model, c, weights, ctx, reps):
     }
     out = {}
     nbytes = kernel_bytes(c, ctx)
+    timer = Timer(rt)
     for name, fn in launches.items():
-        timers = [Timer(rt) for _ in range(L)]
+        fn(0)  # warm the launch path
         samples = []
         for _ in range(reps):
+            # one event pair around L back-to-back launches on the model's
+            # stream (one per layer, distinct weights): average per launch
+            timer.start(stream)
             for l in range(L):
-                timers[l].start(stream)
                 fn(l)
-                timers[l].stop(stream)
-            samples += [t.elapsed_ms() for t in timers]
-        for t in timers:
-            t.close()
-        ms = float(np.mean(samples))
+            timer.stop(stream)
+            samples.append(timer.elapsed_ms() / L)
+        ms = float(np.median(samples))
         out[name] = {"avg_us": round(ms * 1e3, 3), "bytes": nbytes[name],
                      "gbs": round(nbytes[name] / (ms * 1e-3) / 1e9, 1),
                      "frac": round(nbytes[name] / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-                     "launches": len(samples)}
+                     "launches": reps * L}
+    timer.close()
     return out
 
 
@@ -213,6 +216,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU decode for the baseline (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay launches without a graph")
+    ap.add_argument("--split", type=int, default=0,
+                    help="attention split length (0: the library's choice)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path "
@@ -232,7 +237,7 @@ def main():
     log(f"device {rt.info.arch.decode()} cus={rt.info.compute_units}; generating weights")
     t0 = time.time()
     model = ammon_amd.LlamaModel.synthetic(rt, c, seed=2024, std=0.02,
-                                           use_graph=not args.no_graph)
+                                           use_graph=not args.no_graph, split_len=args.split)
     head = c.dim // c.n_heads
     kv_n = c.n_kv_heads * c.max_seq * head
     for l in range(c.n_layers):
@@ -266,7 +271,7 @@ def main():
     log(f"{args.steps} tokens in {ms:.2f} ms (wall {wall * 1e3:.1f} ms): {tps:.1f} tok/s, "
         f"{tok_bytes / (ms_per_step * 1e-3) / 1e9:.0f} GB/s per token stream")
 
-    kernels = time_kernels(rt, model, c, model.weights, ctx_mid, args.kernel_reps)
+    kernels = time_kernels(rt, model, c, model.weights, ctx_mid, args.kernel_reps, args.split)
     for k, v in kernels.items():
         log(f"  {k:18s} {v['avg_us']:9.2f} us  {v['gbs']:7.1f} GB/s  frac {v['frac']:.3f}")
     dom = kernels["gate_up_swiglu"]

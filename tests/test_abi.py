@@ -78,7 +78,8 @@ def test_attention_scratch_geometry():
     assert ammon_amd.attention_scratch_bytes(6, 48, 256, 8) == 6 * 32 * 50 * 4
     split = _abi.lib.ammon_attention_default_split(None, 8, 8192)
     assert 16 <= split <= 1024 and split & (split - 1) == 0
-    assert 8 * ammon_amd.attention_splits(8192, split) <= 4 * 256
+    assert 8 * ammon_amd.attention_splits(8192, split) <= 2 * 256
+    assert split == 128
 
 
 def test_null_runtime_is_a_validation_error():
