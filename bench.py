@@ -60,18 +60,19 @@ def kernel_bytes(c, ctx):
         "qkv_rope_store": (q + 2 * kv) * c.dim * 2 + 4 * c.dim * 2 + 4 * q + 2 * 2 * kv,
         "w2_residual": c.dim * c.hidden * 2 + 4 * c.hidden + 4 * c.dim * 2,
         "wo_residual": c.dim * q * 2 + 4 * q + 4 * c.dim * 2,
-        "attention_partial": 2 * ctx * kv * 2 + 4 * q,
+        "attention_partial": 2 * ctx * kv * 2 + 8 * q,
         "lm_head": c.vocab * c.dim * 2 + 4 * c.dim * 2 + 4 * c.vocab,
     }
 
 
-def time_kernels(rt, model, c, weights, ctx, reps, split=0):
+def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
     """Average duration of each fused kernel: HIP events on the model's
-    stream around batches of back-to-back launches that cycle through all
-    layers' weights, so nothing is served from cache."""
+    stream around batches of L back-to-back launches (one per layer, so
+    nothing is served from cache), replayed as one captured graph unless
+    use_graph is False."""
     import ammon_amd
     from ammon_amd import Timer
-    from ammon_amd._abi import BF16, F32, call
+    from ammon_amd._abi import BF16, F32, call, check, lib
 
     L, head = c.n_layers, c.dim // c.n_heads
     q, kv = head * c.n_heads, head * c.n_kv_heads
@@ -97,41 +98,59 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0):
         return k, v
 
     rms = lambda name, l: ctypes.c_void_p(int(weights[name]) + l * c.dim * 4)
+    # per kernel: the entry point and its arguments for each of the L layers
     launches = {
-        "qkv_rope_store": lambda l: call(
-            "ammon_qkv_rope_store", rt.handle, stream, x, rms("rms_att", l), F32, c.eps,
-            w("wq", l, q * c.dim), w("wk", l, kv * c.dim), w("wv", l, kv * c.dim), BF16, c.dim,
-            c.n_heads, c.n_kv_heads, head, qb, *kv_ptr(l), BF16, c.max_seq, step, table),
-        "attention_partial": lambda l: call(
-            "ammon_attention_partial", rt.handle, stream, qb, c.n_heads, *kv_ptr(l), BF16,
-            c.n_kv_heads, head, c.max_seq, step, split, part),
-        "wo_residual": lambda l: call(
-            "ammon_gemv", rt.handle, stream, w("wo", l, c.dim * q), BF16, c.dim, q, xb, xr, xr),
-        "gate_up_swiglu": lambda l: call(
-            "ammon_gate_up_swiglu", rt.handle, stream, x, rms("rms_ffn", l), F32, c.eps,
-            w("w1", l, c.hidden * c.dim), w("w3", l, c.hidden * c.dim), BF16, c.dim, c.hidden,
-            hb),
-        "w2_residual": lambda l: call(
-            "ammon_gemv", rt.handle, stream, w("w2", l, c.dim * c.hidden), BF16, c.dim,
-            c.hidden, hb, xr, xr),
-        "lm_head": lambda l: call(
-            "ammon_gemv_rmsnorm", rt.handle, stream, x, weights["rms_final"], F32, c.eps,
-            weights["wcls"], BF16, c.vocab, c.dim, logits),
+        "qkv_rope_store": ("ammon_qkv_rope_store", lambda l: (
+            rt.handle, stream, x, rms("rms_att", l), F32, c.eps, w("wq", l, q * c.dim),
+            w("wk", l, kv * c.dim), w("wv", l, kv * c.dim), BF16, c.dim, c.n_heads,
+            c.n_kv_heads, head, qb, *kv_ptr(l), BF16, c.max_seq, step, table)),
+        "attention_partial": ("ammon_attention_partial", lambda l: (
+            rt.handle, stream, qb, c.n_heads, *kv_ptr(l), BF16, c.n_kv_heads, head, c.max_seq,
+            step, split, part)),
+        "wo_residual": ("ammon_gemv", lambda l: (
+            rt.handle, stream, w("wo", l, c.dim * q), BF16, c.dim, q, xb, xr, xr)),
+        "gate_up_swiglu": ("ammon_gate_up_swiglu", lambda l: (
+            rt.handle, stream, x, rms("rms_ffn", l), F32, c.eps, w("w1", l, c.hidden * c.dim),
+            w("w3", l, c.hidden * c.dim), BF16, c.dim, c.hidden, hb)),
+        "w2_residual": ("ammon_gemv", lambda l: (
+            rt.handle, stream, w("w2", l, c.dim * c.hidden), BF16, c.dim, c.hidden, hb, xr,
+            xr)),
+        "lm_head": ("ammon_gemv_rmsnorm", lambda l: (
+            rt.handle, stream, x, weights["rms_final"], F32, c.eps, weights["wcls"], BF16,
+            c.vocab, c.dim, logits)),
     }
     out = {}
     nbytes = kernel_bytes(c, ctx)
     timer = Timer(rt)
-    for name, fn in launches.items():
-        fn(0)  # warm the launch path
+    for name, (entry, args_of) in launches.items():
+        fn = getattr(lib, entry)
+        per_layer = [args_of(l) for l in range(L)]
+
+        def run_layers():
+            for a in per_layer:
+                check(fn(*a))
+
+        graph = None
+        if use_graph:
+            # the L launches as one graph: no host launch overhead between them
+            call("ammon_capture_begin", rt.handle, stream)
+            run_layers()
+            graph = ctypes.c_void_p()
+            call("ammon_capture_end", rt.handle, stream, ctypes.byref(graph))
+            body = lambda: call("ammon_graph_launch", rt.handle, graph, stream)
+        else:
+            body = run_layers
+        body()  # warm the launch path
         samples = []
         for _ in range(reps):
             # one event pair around L back-to-back launches on the model's
             # stream (one per layer, distinct weights): average per launch
             timer.start(stream)
-            for l in range(L):
-                fn(l)
+            body()
             timer.stop(stream)
             samples.append(timer.elapsed_ms() / L)
+        if graph is not None:
+            call("ammon_graph_destroy", rt.handle, graph)
         ms = float(np.median(samples))
         out[name] = {"avg_us": round(ms * 1e3, 3), "bytes": nbytes[name],
                      "gbs": round(nbytes[name] / (ms * 1e-3) / 1e9, 1),
@@ -201,6 +220,46 @@ def cpu_baseline(rt, model, c, weights, start_pos, token0, gpu_tokens, budget_s)
     }
 
 
+TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                            "hbm_traffic_llama3_8b_ctx8192.json")
+
+
+def measured_traffic(kernel, algorithmic_bytes):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 --pmc
+    summary (FETCH_SIZE and WRITE_SIZE passes over this benchmark, each
+    scaled by the counter's reading for the copy probe).  Empty when the
+    summary is missing or was taken on a different shape."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)["kernels"][kernel]
+    except (OSError, KeyError, ValueError):
+        return {}
+    if rec.get("algorithmic_bytes") != algorithmic_bytes:
+        return {}
+    return {"traffic_bytes": rec["traffic_bytes"],
+            "source": "profiles/" + os.path.basename(TRAFFIC_FILE)}
+
+
+COPY_PROBE_N = 1 << 26  # fp32 elements per operand (256 MiB)
+
+
+def copy_probe(rt, reps=4):
+    """out = a + b over COPY_PROBE_N floats: reads 2 * 256 MiB and writes
+    256 MiB per launch.  Under rocprofv3 --pmc its FETCH_SIZE / WRITE_SIZE
+    calibrate the counters' units against a known byte count."""
+    from ammon_amd._abi import F32, call
+    bufs = [rt.alloc(COPY_PROBE_N * 4) for _ in range(3)]
+    for i, b in enumerate(bufs[:2]):
+        rt.fill_normal(b, F32, COPY_PROBE_N, 11, i)
+    for _ in range(reps):
+        call("ammon_add", rt.handle, None, bufs[0], bufs[1], bufs[2], COPY_PROBE_N)
+    rt.synchronize()
+    log(f"copy probe: {reps} x ammon_add over {COPY_PROBE_N} floats "
+        f"(read {8 * COPY_PROBE_N} B, write {4 * COPY_PROBE_N} B per launch)")
+    for b in bufs:
+        b.free()
+
+
 def oracle_layout(head_major, kv_heads, seq, head):
     from ammon_amd import kv_unpermute
     return kv_unpermute(head_major.reshape(kv_heads, seq, head), kv_heads, seq, head)
@@ -218,10 +277,13 @@ def main():
     ap.add_argument("--no-graph", action="store_true", help="replay launches without a graph")
     ap.add_argument("--split", type=int, default=0,
                     help="attention split length (0: the library's choice)")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="also run a plain streaming kernel of known size (ammon_add over "
+                         "256 MiB operands), the calibration for HBM byte counters")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (asked for --gpus {args.gpus}); the decode path "
-              f"is single-device. See DESIGN.md for how it would shard.", file=sys.stderr)
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the decode "
+              f"path here is single-device.", file=sys.stderr)
         sys.exit(2)
 
     import ammon_amd
@@ -248,6 +310,9 @@ def main():
     rt.synchronize()
     log(f"weights + KV prefill in {time.time() - t0:.1f}s; launches/token={model.launches + 2}")
 
+    if args.copy_probe:
+        copy_probe(rt)
+
     token0 = 128000
     stream = model.stream
     # Warmup continues the same greedy chain the timed steps extend; the
@@ -271,10 +336,12 @@ def main():
     log(f"{args.steps} tokens in {ms:.2f} ms (wall {wall * 1e3:.1f} ms): {tps:.1f} tok/s, "
         f"{tok_bytes / (ms_per_step * 1e-3) / 1e9:.0f} GB/s per token stream")
 
-    kernels = time_kernels(rt, model, c, model.weights, ctx_mid, args.kernel_reps, args.split)
+    kernels = time_kernels(rt, model, c, model.weights, ctx_mid, args.kernel_reps, args.split,
+                           use_graph=not args.no_graph)
     for k, v in kernels.items():
         log(f"  {k:18s} {v['avg_us']:9.2f} us  {v['gbs']:7.1f} GB/s  frac {v['frac']:.3f}")
     dom = kernels["gate_up_swiglu"]
+    traffic = measured_traffic("gate_up_swiglu", dom["bytes"])
 
     cpu = None
     if args.cpu_budget > 0 and not args.no_cpu:
@@ -316,7 +383,8 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": dom["frac"],
-            "traffic": None,
+            "traffic": traffic.get("traffic_bytes"),
+            "traffic_source": traffic.get("source"),
             "bytes_per_launch": dom["bytes"],
             "avg_launch_us": dom["avg_us"],
         },
