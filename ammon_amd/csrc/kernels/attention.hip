@@ -7,10 +7,9 @@
 // registers and used for all G heads (the reference re-reads it per q head).
 // A lane owns CH consecutive dims of one position (16-byte loads for bf16
 // head 128), so a wave covers 64 / P2 positions per pass over the head-major
-// cache [kv_heads, seq, head].  Scores land in LDS, the split max and
-// exp-sums are wave reductions, and the V accumulation is reduced across the
-// lanes of a wave (butterfly) and then across the four waves (LDS, wave
-// order).  Writes partial[h, s, :] = (sum_t e^{score_t - m} V_t, m, l) with
+// cache [kv_heads, seq, head].  Each group of lanes keeps an online softmax
+// over the positions it sees; the groups are merged once at the end (LDS).
+// Writes partial[h, s, :] = (sum_t e^{score_t - m} V_t, m, l) with
 // the reference's layout [q_heads, splits, head + 2].  Splits that start past
 // pos write nothing.
 //
@@ -22,7 +21,6 @@
 #include "device_common.h"
 
 #define ATT_ROUNDS 4         // position rounds per chunk held in registers
-#define ATT_CHUNK_MAX (ATT_ROUNDS * AMMON_WAVES * 32)  // positions per chunk, P2 >= 2
 #define ATT_MAX_SPLITS 4096
 #define ATT_MAX_HEAD 128
 
@@ -36,15 +34,15 @@ AMMON_DEV float group_sum(float v, uint32_t width) {
 
 // One workgroup = one (split, kv head).  The split's positions are processed
 // in chunks of ATT_ROUNDS rounds; a round is 4 waves x (64 / P2) positions,
-// P2 lanes per position (the power of two >= head / CH).  Chunks are
+// P2 lanes per position (the power of two >= head / CH), so each group of P2
+// lanes -- a "slot" -- sees one position per round.  Chunks are
 // double-buffered in registers: the next chunk's K and V loads are in flight
-// while the current one is processed.  For a chunk, the raw q.k dots go to
-// LDS, each wave turns one query head's dots into scores (the reference's
-// division by sqrt(head)), max and exp-sum, and the V chunk is accumulated
-// with the probabilities.  Chunks merge online (running max and sum per
-// head, uniform across the workgroup), so a split of any length is one pass;
-// with a single chunk the merge scales by exactly 1.  The per-lane V sums
-// are reduced across position slots and waves in LDS.
+// while the current one is processed.  After the q.k reduction every lane of
+// a slot holds its position's score (the reference's dot / sqrt(head)), so
+// each slot runs its own online softmax (running max, exp-sum and V
+// accumulator per query head) with no LDS traffic and no barrier inside the
+// split.  At the end the slots' states are merged through LDS: M = max of
+// the slot maxima, acc = sum_s acc_s e^{m_s - M}, l = sum_s l_s e^{m_s - M}.
 // HEAD > 0 fixes the head width at compile time (then the lane layout and
 // the DPP reduction steps are constants); EXACT_G means q_heads / kv_heads
 // equals GMAX.  The generic instantiations (HEAD 0) read both at run time.
@@ -68,14 +66,11 @@ constexpr uint32_t ceil_pow2(uint32_t v) {
 template <typename KV, int CH, int GMAX, int HEAD, bool EXACT_G>
 AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
   constexpr int R = ATT_ROUNDS;
-  // Probabilities of the current chunk, and after the last chunk the
-  // cross-slot reduction area (one padded row of GMAX * CH floats per lane).
-  constexpr int P_FLOATS = GMAX * ATT_CHUNK_MAX;
-  constexpr int RED_FLOATS = AMMON_WG * (GMAX * CH + 1);
-  __shared__ float s_lds[P_FLOATS > RED_FLOATS ? P_FLOATS : RED_FLOATS];
-  __shared__ float s_ml[2][GMAX];
-  float(*s_p)[ATT_CHUNK_MAX] = (float(*)[ATT_CHUNK_MAX])s_lds;
-  float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])s_lds;
+  // per-lane accumulators of the final cross-slot merge (one padded row of
+  // GMAX * CH floats per lane) and the slots' (m, l) per head
+  __shared__ float s_red[AMMON_WG][GMAX * CH + 1];
+  __shared__ float s_m[AMMON_WG / 2][GMAX];
+  __shared__ float s_l[AMMON_WG / 2][GMAX];
 
   const uint32_t split = blockIdx.x, g = blockIdx.y;
   const uint32_t pos = p.step->position;
@@ -97,10 +92,38 @@ AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
   const uint32_t sub = lane & (P2 - 1), slot = lane / P2;
   const bool active = sub < LP;
   const uint32_t round = AMMON_WAVES * PW;
-  const uint32_t chunk = R * round;  // <= ATT_CHUNK_MAX since P2 >= 2
+  const uint32_t chunk = R * round;
   using C = Chunk<KV, CH>;
   using QC = Chunk<float, (CH >= 4 ? 4 : CH)>;
   constexpr int QCH = CH >= 4 ? 4 : CH;
+
+  // Buffer resources over this split's valid positions: inactive lanes and
+  // positions past the split read zero through an out-of-range offset.
+  const uint32_t es = (uint32_t)sizeof(KV);
+  const __amdgpu_buffer_rsrc_t kres =
+      make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
+  const __amdgpu_buffer_rsrc_t vres =
+      make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
+  // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
+  // per weight (results below 2^-126 flush to zero, far below fp32
+  // resolution of the sums).  The running maxima are kept in base-2 units
+  // and converted back (x ln 2) when the partial is written.
+  const float scale2 = 1.4426950408889634f / sqrtf((float)head);
+
+  using VT = typename C::V;
+  auto load_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const uint32_t t = c0 + r * round + wave * PW + slot;
+      const uint32_t off = (t < n && active) ? (t * head + sub * CH) * es : AMMON_OOB;
+      kr[r] = C::load_buf(kres, off);
+      vr[r] = C::load_buf(vres, off);
+    }
+  };
+  // K and V of the first two chunks are requested before q is read.
+  VT kA[R], vA[R], kB[R], vB[R];
+  load_chunk(0, kA, vA);
+  load_chunk(chunk, kB, vB);
 
   float qr[GMAX][CH];
 #pragma unroll
@@ -116,15 +139,6 @@ AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
     }
   }
 
-  // Buffer resources over this split's valid positions: inactive lanes and
-  // positions past the chunk read zero through an out-of-range offset.
-  const uint32_t es = (uint32_t)sizeof(KV);
-  const __amdgpu_buffer_rsrc_t kres =
-      make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  const __amdgpu_buffer_rsrc_t vres =
-      make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  const float root = sqrtf((float)head);
-
   float acc[GMAX][CH];
   float m_run[GMAX], l_run[GMAX];
 #pragma unroll
@@ -135,104 +149,57 @@ AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
     for (int c = 0; c < CH; ++c) acc[j][c] = 0.f;
   }
 
-  // Chunk pipeline: two register buffers of K and V; while one chunk is
-  // scored and accumulated the next one's loads are in flight.
-  using VT = typename C::V;
-  auto load_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
-    const uint32_t cn = c0 < n ? min(chunk, n - c0) : 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t tl = r * round + wave * PW + slot;
-      const uint32_t off = (tl < cn && active) ? ((c0 + tl) * head + sub * CH) * es : AMMON_OOB;
-      kr[r] = C::load_buf(kres, off);
-      vr[r] = C::load_buf(vres, off);
-    }
-  };
   auto compute_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
-    const uint32_t cn = min(chunk, n - c0);
-    if (c0 > 0) __syncthreads();  // previous chunk's probabilities consumed
-
-    // raw q.k dots: this lane's CH dims, then the P2 lanes of the position
+    // scores of this slot's R positions (-inf past the split)
+    float sc[R][GMAX];
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t tl = r * round + wave * PW + slot;
+      const uint32_t t = c0 + r * round + wave * PW + slot;
       float kf[CH];
       C::widen(kr[r], kf);
 #pragma unroll
       for (int j = 0; j < GMAX; ++j) {
-        float sacc = 0.f;
+        float d = 0.f;
 #pragma unroll
-        for (int c = 0; c < CH; ++c) sacc += qr[j][c] * kf[c];
+        for (int c = 0; c < CH; ++c) d += qr[j][c] * kf[c];
         if constexpr (HEAD > 0)
-          sacc = group_sum_c<P2C>(sacc);
+          d = group_sum_c<P2C>(d);
         else
-          sacc = group_sum(sacc, P2);
-        if (sub == 0 && tl < cn && (uint32_t)j < G) s_p[j][tl] = sacc;
+          d = group_sum(d, P2);
+        // score (reference src/kernels.rs:298: dot / sqrt(head)) in base-2
+        // units: d * log2(e) / sqrt(head)
+        sc[r][j] = t < n ? d * scale2 : -INFINITY;
       }
     }
-    __syncthreads();
-
-    // scores = dot / sqrt(head) (reference src/kernels.rs:298), chunk max
-    // and exp-sum per query head (one wave per head)
-    for (uint32_t j = wave; j < G; j += AMMON_WAVES) {
-      float m = -INFINITY;
-      for (uint32_t t = lane; t < cn; t += 64) {
-        const float sc = s_p[j][t] / root;
-        s_p[j][t] = sc;
-        m = fmaxf(m, sc);
-      }
-      m = wave_max(m);
-      float l = 0.f;
-      for (uint32_t t = lane; t < cn; t += 64) {
-        const float e = expf(s_p[j][t] - m);
-        s_p[j][t] = e;
-        l += e;
-      }
-      l = wave_sum(l);
-      if (lane == 0) {
-        s_ml[0][j] = m;
-        s_ml[1][j] = l;
-      }
-    }
-    __syncthreads();
-
-    // online merge with the previous chunks, then accumulate V
-    float scale[GMAX];
+    // online softmax update of the slot's state
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) {
-      scale[j] = 0.f;
-      if ((uint32_t)j < G) {
-        const float cm = s_ml[0][j], cl = s_ml[1][j];
-        const float M = fmaxf(m_run[j], cm);
-        const float a = expf(m_run[j] - M), b = expf(cm - M);
-        if (c0 > 0)
+      if (!EXACT_G && (uint32_t)j >= G) continue;
+      float mc = m_run[j];
 #pragma unroll
-          for (int c = 0; c < CH; ++c) acc[j][c] *= a;
-        l_run[j] = l_run[j] * a + cl * b;
-        m_run[j] = M;
-        scale[j] = b;
-      }
-    }
+      for (int r = 0; r < R; ++r) mc = fmaxf(mc, sc[r][j]);
+      if (mc == -INFINITY) continue;  // nothing seen yet
+      const float a = __builtin_amdgcn_exp2f(m_run[j] - mc);
+      float l = l_run[j] * a;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t tl = r * round + wave * PW + slot;
-      if (tl < cn) {
+      for (int c = 0; c < CH; ++c) acc[j][c] *= a;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float e = __builtin_amdgcn_exp2f(sc[r][j] - mc);  // 0 for -inf scores
+        l += e;
         float vf[CH];
         C::widen(vr[r], vf);
 #pragma unroll
-        for (int j = 0; j < GMAX; ++j) {
-          const float pj = ((uint32_t)j < G) ? s_p[j][tl] * scale[j] : 0.f;
-#pragma unroll
-          for (int c = 0; c < CH; ++c) acc[j][c] += pj * vf[c];
-        }
+        for (int c = 0; c < CH; ++c) acc[j][c] += e * vf[c];
       }
+      l_run[j] = l;
+      m_run[j] = mc;
     }
   };
 
-  VT kA[R], vA[R], kB[R], vB[R];
-  load_chunk(0, kA, vA);
-  load_chunk(chunk, kB, vB);
   for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
+    // loads past the split read zero without touching memory, so they are
+    // issued unconditionally and the wait counts stay exact
     compute_chunk(c0, kA, vA);
     load_chunk(c0 + 2 * chunk, kA, vA);
     if (c0 + chunk >= n) break;
@@ -240,32 +207,42 @@ AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
     load_chunk(c0 + 3 * chunk, kB, vB);
   }
 
-  // reduce acc over the 4 * PW position slots of the workgroup through LDS
-  // (the probability area is reused: wait until every wave is done with it)
-  __syncthreads();
+  // merge the 4 * PW slots of the workgroup through LDS
 #pragma unroll
   for (int j = 0; j < GMAX; ++j)
 #pragma unroll
     for (int c = 0; c < CH; ++c) s_red[threadIdx.x][j * CH + c] = acc[j][c];
+  const uint32_t slots = AMMON_WAVES * PW;
+  const uint32_t slot_id = wave * PW + slot;
+  if (sub == 0) {
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      s_m[slot_id][j] = m_run[j];
+      s_l[slot_id][j] = l_run[j];
+    }
+  }
   __syncthreads();
   const uint32_t slot_w = head + 2;
-  const uint32_t slots = AMMON_WAVES * PW;
   for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
     const uint32_t j = idx / head, d = idx - j * head;
     const uint32_t sb = d / CH, c = d % CH;  // lane sub and element (CH is a constant)
-    float total = 0.f;
+    float M = -INFINITY;
+    for (uint32_t s = 0; s < slots; ++s) M = fmaxf(M, s_m[s][j]);
+    float total = 0.f, L = 0.f;
     for (uint32_t s = 0; s < slots; ++s) {
+      const float ms = s_m[s][j];
+      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
       // thread of (wave s / PW, slot s % PW, sub sb)
       const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
-      total += s_red[t][j * CH + c];
+      total += s_red[t][j * CH + c] * w;
+      L += s_l[s][j] * w;
     }
-    p.partial[((size_t)(g * G + j) * p.splits + split) * slot_w + d] = total;
-  }
-  if (threadIdx.x < G) {
-    const uint32_t j = threadIdx.x;
     float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
-    o[head] = m_run[j];
-    o[head + 1] = l_run[j];
+    o[d] = total;
+    if (d == 0) {
+      o[head] = M * 0.6931471805599453f;  // back to natural-log units
+      o[head + 1] = L;
+    }
   }
 }
 
