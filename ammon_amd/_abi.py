@@ -108,7 +108,8 @@ class LlamaConfig(ctypes.Structure):
     _fields_ = [("dim", _U32), ("n_layers", _U32), ("n_heads", _U32), ("n_kv_heads", _U32),
                 ("hidden", _U32), ("vocab", _U32), ("max_seq", _U32), ("theta", _F),
                 ("eps", _F), ("w_dtype", ctypes.c_int), ("kv_dtype", ctypes.c_int),
-                ("use_graph", _U32), ("split_len", _U32)]
+                ("use_graph", _U32), ("split_len", _U32),
+                ("persistent", _U32)]
 
 
 class LlamaWeights(ctypes.Structure):

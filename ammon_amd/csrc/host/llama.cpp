@@ -21,6 +21,153 @@
 namespace ammon {
 namespace {
 
+// One cooperative launch per token (kernels/token.hip): the same arithmetic
+// as the launch list, with grid barriers instead of kernel boundaries.
+class PersistentToken {
+ public:
+  // bf16 weights, head 128, 16-byte-aligned rows, 1/2/4/8 q heads per kv head.
+  static bool supported(const ammon_llama_config &c, uint32_t head) {
+    const uint32_t g = c.n_kv_heads ? c.n_heads / c.n_kv_heads : 0;
+    return c.w_dtype == AMMON_BF16 && head == 128 && (g == 1 || g == 2 || g == 4 || g == 8) &&
+           c.dim % 8 == 0 && c.hidden % 8 == 0 && (c.kv_dtype == AMMON_BF16 || c.kv_dtype == AMMON_F32);
+  }
+
+  PersistentToken(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w,
+                  const KvCache &cache, uint32_t split_len, const Tensor &logits,
+                  const Tensor &step, const Tensor &prompt, const Tensor &tokens, const float *table)
+      : rt_(rt) {
+    ammon_runtime *raw = rt.raw();
+    const uint32_t head = c.dim / c.n_heads, g = c.n_heads / c.n_kv_heads;
+    const int gi = g == 1 ? 0 : g == 2 ? 1 : g == 4 ? 2 : 3;
+    const int di = c.kv_dtype == AMMON_BF16 ? 1 : 0;
+    f_ = raw->k.token[di][gi];
+    if (!f_) throw Error(AMMON_E_HIP, "persistent token kernel not loaded");
+    const uint32_t q_dim = c.n_heads * head;
+    const uint32_t splits = ammon_attention_splits(c.max_seq, split_len);
+    // dynamic LDS: x staged for the widest GEMV input, or an attention /
+    // combine / argmax unit, whichever is larger
+    const uint32_t tile = 64 * ammon_rt::kGemvTileChunks * 8;
+    auto padded = [&](uint32_t n) { return (n + tile - 1) / tile * tile; };
+    const uint32_t xs = std::max(std::max(padded(c.dim), padded(c.hidden)), padded(q_dim));
+    const uint32_t ach = c.kv_dtype == AMMON_BF16 ? 8 : 4;
+    const uint32_t att = 256 * (g * ach + 1) + 2 * 128 * g;
+    const uint32_t comb = 64 * 33 + 64 + 4;
+    shmem_ = 4 * std::max(std::max(xs, att), std::max(comb, 512u));
+    const uint32_t occ = ammon_rt::occupancy(raw, f_, shmem_);
+    if (occ == 0) throw Error(AMMON_E_HIP, "persistent token kernel does not fit on a CU");
+    grid_ = (uint32_t)raw->info.compute_units * std::min(occ, 2u);
+
+    // one slice per phase and layer, each a whole number of 256-byte lines
+    auto line = [](uint64_t floats) { return (uint32_t)((floats + 63) / 64 * 64); };
+    const uint32_t L = c.n_layers;
+    const uint32_t xs_stride = line(c.dim), q_stride = line(q_dim), hb_stride = line(c.hidden);
+    const uint32_t part_stride =
+        line(ammon_attention_scratch_bytes(c.n_heads, head, c.max_seq, split_len) / 4);
+    x_ = Tensor::zeros(rt, Shape::vector((2 * L + 1) * xs_stride), DType::F32);
+    q_ = Tensor::zeros(rt, Shape::vector(L * q_stride), DType::F32);
+    att_ = Tensor::zeros(rt, Shape::vector(L * q_stride), DType::F32);
+    hb_ = Tensor::zeros(rt, Shape::vector(L * hb_stride), DType::F32);
+    partial_ = Tensor::zeros(rt, Shape::vector(L * part_stride), DType::F32);
+    cand_v_ = Tensor::zeros(rt, Shape::vector(grid_), DType::F32);
+    cand_i_ = Tensor::zeros(rt, Shape::vector(grid_), DType::U32);
+    sync_ = Tensor::zeros(rt, Shape::vector(AMMON_TOKEN_SYNC_WORDS), DType::U32);
+
+    ammon_k_token &p = p_;
+    p = ammon_k_token{};
+    p.tok_emb = w.tok_emb;
+    p.rms_att = w.rms_att;
+    p.rms_ffn = w.rms_ffn;
+    p.wq = w.wq;
+    p.wk = w.wk;
+    p.wv = w.wv;
+    p.wo = w.wo;
+    p.w1 = w.w1;
+    p.w3 = w.w3;
+    p.w2 = w.w2;
+    p.rms_final = w.rms_final;
+    p.wcls = w.wcls;
+    p.k_cache = cache.layer(0).key.data();
+    p.v_cache = cache.layer(0).value.data();
+    p.table = table;
+    p.step = (ammon_k_step *)step.data();
+    p.x = (float *)x_.data();
+    p.x_stride = xs_stride;
+    p.q_stride = q_stride;
+    p.hb_stride = hb_stride;
+    p.partial_stride = part_stride;
+    p.q = (float *)q_.data();
+    p.att = (float *)att_.data();
+    p.hb = (float *)hb_.data();
+    p.partial = (float *)partial_.data();
+    p.logits = (float *)logits.data();
+    p.cand_v = (float *)cand_v_.data();
+    p.cand_i = (uint32_t *)cand_i_.data();
+    p.sync = (uint32_t *)sync_.data();
+    p.dim = c.dim;
+    p.n_layers = c.n_layers;
+    p.q_heads = c.n_heads;
+    p.kv_heads = c.n_kv_heads;
+    p.head = head;
+    p.hidden = c.hidden;
+    p.vocab = c.vocab;
+    p.seq = c.max_seq;
+    p.split_len = split_len;
+    p.splits = splits;
+    p.eps = c.eps;
+    // a barrier polls about once per microsecond: give up after ~0.2 s
+    p.spin_limit = 200000;
+    prompt_ = (const int32_t *)prompt.data();
+    tokens_ = (int32_t *)tokens.data();
+    max_tokens_ = c.max_seq;
+  }
+
+  // Enqueue one token on `s`.  greedy: argmax + prompt forcing + DecodeStep
+  // update on the device (n_prompt forced tokens from the prompt buffer).
+  void launch(ammon_stream s, bool greedy, uint32_t n_prompt) {
+    ammon_k_token p = p_;
+    p.greedy = greedy ? 1u : 0u;
+    p.prompt = greedy && n_prompt ? prompt_ : nullptr;
+    p.n_prompt = greedy ? n_prompt : 0u;
+    p.tokens = greedy ? tokens_ : nullptr;
+    p.max_tokens = max_tokens_;
+    void *args[] = {&p};
+    ammon_rt::DeviceScope scope(rt_.raw()->device);
+    const hipError_t e = hipModuleLaunchCooperativeKernel(
+        f_, grid_, 1, 1, ammon_rt::kWorkgroup, 1, 1, shmem_,
+        s ? (hipStream_t)s : rt_.raw()->stream, args);
+    if (e != hipSuccess)
+      throw Error(AMMON_E_HIP, std::string("persistent token launch: ") + hipGetErrorString(e));
+  }
+
+  // After the stream has drained: fail if a grid barrier timed out.
+  void check(ammon_stream s) const {
+    uint32_t err = 0;
+    ammon::check(ammon_memcpy(rt_.raw(), &err, (const uint32_t *)sync_.data() + AMMON_TOKEN_SYNC_ERR,
+                              sizeof err, AMMON_COPY_D2H, s),
+                 "persistent token");
+    ammon::check(ammon_stream_synchronize(rt_.raw(), s), "persistent token");
+    if (err) {
+      // results of that launch are invalid; clear the counters for the next
+      ammon::check(ammon_fill(rt_.raw(), s, sync_.data(), AMMON_F32, AMMON_TOKEN_SYNC_WORDS, 0.f),
+                   "persistent token");
+      ammon::check(ammon_stream_synchronize(rt_.raw(), s), "persistent token");
+      throw Error(AMMON_E_HIP,
+                  "persistent token kernel: a grid barrier timed out (workgroups not co-resident)");
+    }
+  }
+
+  uint32_t grid() const { return grid_; }
+
+ private:
+  Runtime rt_;
+  hipFunction_t f_ = nullptr;
+  uint32_t grid_ = 0, shmem_ = 0, max_tokens_ = 0;
+  ammon_k_token p_ = {};
+  const int32_t *prompt_ = nullptr;
+  int32_t *tokens_ = nullptr;
+  Tensor x_, q_, att_, hb_, partial_, cand_v_, cand_i_, sync_;
+};
+
 class LlamaModel : public AutoregressiveModel {
  public:
   LlamaModel(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w);
@@ -37,7 +184,9 @@ class LlamaModel : public AutoregressiveModel {
   void read_tokens(uint32_t start, uint32_t n, int32_t *out);
   ammon_stream stream() const { return stream_; }
   float *device_logits() const { return (float *)logits_.data(); }
-  uint32_t launches() const { return (uint32_t)token_scheme_->ir_node_count(); }
+  uint32_t launches() const {
+    return persistent_ ? 1u : (uint32_t)token_scheme_->ir_node_count();
+  }
   // Host logits of the most recent step() (what generate_tokens last saw).
   const std::vector<float> &last_logits() const { return host_logits_; }
 
@@ -60,6 +209,8 @@ class LlamaModel : public AutoregressiveModel {
   Tensor x_, logits_, step_, prompt_, tokens_, scratch_;
   ammon_stream stream_ = nullptr;  // both schemes replay here, in order
   std::unique_ptr<Scheme> token_scheme_, decode_scheme_;
+  std::unique_ptr<PersistentToken> persistent_;
+  Tensor rope_table_;
   uint32_t decode_prompt_ = 0xffffffffu;
   ammon_decode_step *pinned_step_ = nullptr;
   float *pinned_logits_ = nullptr;
@@ -131,6 +282,14 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
   check(ammon_stream_create(rt.raw(), &stream_), "llama stream");
   token_scheme_ = std::make_unique<Scheme>(rt, c.use_graph != 0, stream_);
   record_token(*token_scheme_);
+  if (c.persistent && PersistentToken::supported(c, head_)) {
+    std::vector<float> table(ammon_rope_table_bytes(head_, c.max_seq) / sizeof(float));
+    check(ammon_rope_table_host(c.theta, head_, c.max_seq, table.data()), "rope table");
+    rope_table_ = Tensor::from_f32(rt, Shape::vector((uint32_t)table.size()), table);
+    persistent_ = std::make_unique<PersistentToken>(
+        rt, c, w, cache_, attn_.split_len_for(c.n_kv_heads), logits_, step_, prompt_, tokens_,
+        (const float *)rope_table_.data());
+  }
 }
 
 LlamaModel::~LlamaModel() {
@@ -179,13 +338,16 @@ const std::vector<float> &LlamaModel::step(uint32_t token, uint32_t pos) {
   if (pos >= c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "step: position " + std::to_string(pos) + " >= max_seq " +
                                         std::to_string(c_.max_seq));
-  Scheme &s = *token_scheme_;
-  deposit(token, pos, s.stream());
-  s.submit();
+  deposit(token, pos, stream_);
+  if (persistent_)
+    persistent_->launch(stream_, false, 0);
+  else
+    token_scheme_->submit();
   check(ammon_memcpy(rt_.raw(), pinned_logits_, logits_.data(), sizeof(float) * c_.vocab,
-                     AMMON_COPY_D2H, s.stream()),
+                     AMMON_COPY_D2H, stream_),
         "logits");
-  s.synchronize();
+  check(ammon_stream_synchronize(rt_.raw(), stream_), "step");
+  if (persistent_) persistent_->check(stream_);
   std::memcpy(host_logits_.data(), pinned_logits_, sizeof(float) * c_.vocab);
   return host_logits_;
 }
@@ -200,21 +362,25 @@ GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prom
   const uint32_t limit = std::min(max_new, c_.max_seq);
   const uint32_t steps = limit > 0 ? limit - 1 : 0;
   const uint32_t n_prompt = (uint32_t)std::min<size_t>(prompt.size(), c_.max_seq);
-  ensure_decode_scheme(n_prompt);
-  Scheme &s = *decode_scheme_;
+  if (!persistent_) ensure_decode_scheme(n_prompt);
+  ammon_stream st = stream_;
   check(ammon_memcpy(rt_.raw(), prompt_.data(), prompt.data(), sizeof(int32_t) * n_prompt,
-                     AMMON_COPY_H2D, s.stream()),
+                     AMMON_COPY_H2D, st),
         "prompt upload");
-  deposit((uint32_t)prompt[0], 0, s.stream());
+  deposit((uint32_t)prompt[0], 0, st);
   ammon_event e0 = nullptr, e1 = nullptr;
   check(ammon_event_create(rt_.raw(), &e0), "event");
   check(ammon_event_create(rt_.raw(), &e1), "event");
   for (uint32_t i = 0; i < steps; ++i) {
-    s.submit();
-    if (i == 0) check(ammon_event_record(rt_.raw(), e0, s.stream()), "event");
+    if (persistent_)
+      persistent_->launch(st, true, n_prompt);
+    else
+      decode_scheme_->submit();
+    if (i == 0) check(ammon_event_record(rt_.raw(), e0, st), "event");
   }
-  check(ammon_event_record(rt_.raw(), e1, s.stream()), "event");
-  s.synchronize();
+  check(ammon_event_record(rt_.raw(), e1, st), "event");
+  check(ammon_stream_synchronize(rt_.raw(), st), "generate");
+  if (persistent_) persistent_->check(st);
   float ms = 0.f;
   if (steps > 1) check(ammon_event_elapsed_ms(rt_.raw(), e0, e1, &ms), "event");
   ammon_event_destroy(rt_.raw(), e0);
@@ -223,13 +389,13 @@ GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prom
   std::vector<int32_t> all(steps);
   if (steps)
     check(ammon_memcpy(rt_.raw(), all.data(), tokens_.data(), sizeof(int32_t) * steps,
-                       AMMON_COPY_D2H, s.stream()),
+                       AMMON_COPY_D2H, st),
           "tokens");
   if (last_logits)
     check(ammon_memcpy(rt_.raw(), last_logits, logits_.data(), sizeof(float) * c_.vocab,
-                       AMMON_COPY_D2H, s.stream()),
+                       AMMON_COPY_D2H, st),
           "logits");
-  s.synchronize();
+  check(ammon_stream_synchronize(rt_.raw(), st), "generate");
   GenerateTokenOutput out;
   out.prompt_tokens = prompt.size();
   for (int32_t t : all) {
@@ -244,15 +410,20 @@ void LlamaModel::decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, in
   if (token >= c_.vocab) throw Error(AMMON_E_VALIDATION, "decode: token outside the vocab");
   if ((uint64_t)start_pos + n_steps > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "decode: start_pos + n_steps exceeds max_seq");
-  ensure_decode_scheme(0);
-  Scheme &s = *decode_scheme_;
-  deposit(token, start_pos, s.stream());
-  for (uint32_t i = 0; i < n_steps; ++i) s.submit();
+  if (!persistent_) ensure_decode_scheme(0);
+  deposit(token, start_pos, stream_);
+  for (uint32_t i = 0; i < n_steps; ++i) {
+    if (persistent_)
+      persistent_->launch(stream_, true, 0);
+    else
+      decode_scheme_->submit();
+  }
   if (tokens) {
     check(ammon_memcpy(rt_.raw(), tokens, (int32_t *)tokens_.data() + start_pos,
-                       sizeof(int32_t) * n_steps, AMMON_COPY_D2H, s.stream()),
+                       sizeof(int32_t) * n_steps, AMMON_COPY_D2H, stream_),
           "tokens");
-    s.synchronize();
+    check(ammon_stream_synchronize(rt_.raw(), stream_), "decode");
+    if (persistent_) persistent_->check(stream_);
   }
 }
 
@@ -260,6 +431,7 @@ void LlamaModel::read_tokens(uint32_t start, uint32_t n, int32_t *out) {
   if ((uint64_t)start + n > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "tokens: range exceeds max_seq");
   check(ammon_stream_synchronize(rt_.raw(), stream_), "tokens");
+  if (persistent_) persistent_->check(stream_);
   if (!n) return;
   check(ammon_memcpy(rt_.raw(), out, (int32_t *)tokens_.data() + start, sizeof(int32_t) * n,
                      AMMON_COPY_D2H, stream_),

@@ -121,6 +121,43 @@ typedef struct {
   uint32_t bits; /* fill: raw 32-bit pattern (f32) or 16-bit (bf16) */
 } ammon_k_fill;
 
+/* Persistent decode-token kernel: one cooperative launch runs a whole decode
+ * token (embed, every layer, final norm + LM head, optionally the greedy
+ * step) with grid-wide barriers between dependent phases.  Per-layer weights
+ * are stacked [L, ...]; the caches are [L, kv_heads, seq, head]; sync must
+ * not be shared by launches that can run at the same time. */
+#define AMMON_TOKEN_SYNC_WORDS 640 /* barrier counters (10 x 64 words)      */
+#define AMMON_TOKEN_SYNC_ERR (64 * 9) /* word set when a barrier timed out */
+typedef struct {
+  const void *tok_emb;                 /* [vocab, dim] */
+  const float *rms_att, *rms_ffn;      /* [L, dim] fp32 */
+  const void *wq, *wk, *wv, *wo;       /* [L, q_dim, dim], [L, kv_dim, dim] x2, [L, dim, q_dim] */
+  const void *w1, *w3, *w2;            /* [L, hidden, dim] x2, [L, dim, hidden] */
+  const float *rms_final;              /* [dim] fp32 */
+  const void *wcls;                    /* [vocab, dim] */
+  void *k_cache, *v_cache;             /* [L, kv_heads, seq, head] */
+  const float *table;                  /* RoPE cos/sin [seq, head/2, 2] */
+  ammon_k_step *step;                  /* token/position; advanced by the greedy step */
+  /* Activations, one slice per phase so no address is written after another
+   * workgroup has read it within a launch: x [2L + 1][x_stride] (embed, then
+   * after each attention / FFN residual), q, att [L][q_stride], hb
+   * [L][hb_stride], partial [L][partial_stride]; logits [vocab]. */
+  float *x, *q, *att, *hb, *partial, *logits;
+  uint32_t x_stride, q_stride, hb_stride, partial_stride;
+  float *cand_v;                       /* [gridDim.x] argmax candidates */
+  uint32_t *cand_i;
+  uint32_t *sync;                      /* AMMON_TOKEN_SYNC_WORDS, zero between launches */
+  const int32_t *prompt;               /* greedy: forced tokens, or NULL */
+  int32_t *tokens;                     /* greedy: tokens[pos] = next, or NULL */
+  int32_t *argmax_out;                 /* greedy: the argmax, or NULL */
+  uint32_t dim, n_layers, q_heads, kv_heads, head, hidden, vocab, seq;
+  uint32_t split_len, splits;
+  uint32_t greedy, n_prompt, max_tokens;
+  uint32_t spin_limit;                 /* polls per barrier before giving up */
+  float eps;
+} ammon_k_token;
+
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,254 +1,12 @@
-// attention.hip -- split-K decode attention with GQA head sharing and a
-// log-sum-exp merge (reference flash-decoding pair, src/kernels.rs:228-410).
-//
-// Pass 1, one workgroup per (split s, kv head g): positions
-// [s*S, s*S + S) clipped to t <= pos, for all G = q_heads / kv_heads query
-// heads of that kv head.  Each K and V byte is loaded once from HBM into
-// registers and used for all G heads (the reference re-reads it per q head).
-// A lane owns CH consecutive dims of one position (16-byte loads for bf16
-// head 128), so a wave covers 64 / P2 positions per pass over the head-major
-// cache [kv_heads, seq, head].  Each group of lanes keeps an online softmax
-// over the positions it sees; the groups are merged once at the end (LDS).
-// Writes partial[h, s, :] = (sum_t e^{score_t - m} V_t, m, l) with
-// the reference's layout [q_heads, splits, head + 2].  Splits that start past
-// pos write nothing.
-//
-// Pass 2, one workgroup per q head: M = max m_s over live splits,
-// out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
-//
-// The reference uses fixed 8-position splits (src/kernels.rs:228-229); here
-// the split length is a launch parameter chosen to fill the device.
-#include "device_common.h"
-
-#define ATT_ROUNDS 4         // position rounds per chunk held in registers
-#define ATT_MAX_SPLITS 4096
-#define ATT_MAX_HEAD 128
-
-// Sum over aligned groups of `width` lanes (a power of two <= 64): DPP
-// inside 16-lane rows, shuffles across rows.
-AMMON_DEV float group_sum(float v, uint32_t width) {
-  v = group_sum16(v, width < 16 ? width : 16);
-  for (uint32_t off = 16; off < width; off <<= 1) v += __shfl_xor(v, off, 64);
-  return v;
-}
-
-// One workgroup = one (split, kv head).  The split's positions are processed
-// in chunks of ATT_ROUNDS rounds; a round is 4 waves x (64 / P2) positions,
-// P2 lanes per position (the power of two >= head / CH), so each group of P2
-// lanes -- a "slot" -- sees one position per round.  Chunks are
-// double-buffered in registers: the next chunk's K and V loads are in flight
-// while the current one is processed.  After the q.k reduction every lane of
-// a slot holds its position's score (the reference's dot / sqrt(head)), so
-// each slot runs its own online softmax (running max, exp-sum and V
-// accumulator per query head) with no LDS traffic and no barrier inside the
-// split.  At the end the slots' states are merged through LDS: M = max of
-// the slot maxima, acc = sum_s acc_s e^{m_s - M}, l = sum_s l_s e^{m_s - M}.
-// HEAD > 0 fixes the head width at compile time (then the lane layout and
-// the DPP reduction steps are constants); EXACT_G means q_heads / kv_heads
-// equals GMAX.  The generic instantiations (HEAD 0) read both at run time.
-template <int W> AMMON_DEV float group_sum_c(float v) {
-  static_assert(W >= 2 && W <= 64 && (W & (W - 1)) == 0, "power of two");
-  v += dpp_get<AMMON_DPP_XOR1>(v);
-  if (W >= 4) v += dpp_get<AMMON_DPP_XOR2>(v);
-  if (W >= 8) v += dpp_get<AMMON_DPP_HALF_MIRROR>(v);
-  if (W >= 16) v += dpp_get<AMMON_DPP_MIRROR>(v);
-  if (W >= 32) v += __shfl_xor(v, 16, 64);
-  if (W >= 64) v += __shfl_xor(v, 32, 64);
-  return v;
-}
-
-constexpr uint32_t ceil_pow2(uint32_t v) {
-  uint32_t p = 2;
-  while (p < v) p <<= 1;
-  return p;
-}
-
-template <typename KV, int CH, int GMAX, int HEAD, bool EXACT_G>
-AMMON_DEV void attention_partial_body(const ammon_k_attention &p) {
-  constexpr int R = ATT_ROUNDS;
-  // per-lane accumulators of the final cross-slot merge (one padded row of
-  // GMAX * CH floats per lane) and the slots' (m, l) per head
-  __shared__ float s_red[AMMON_WG][GMAX * CH + 1];
-  __shared__ float s_m[AMMON_WG / 2][GMAX];
-  __shared__ float s_l[AMMON_WG / 2][GMAX];
-
-  const uint32_t split = blockIdx.x, g = blockIdx.y;
-  const uint32_t pos = p.step->position;
-  if (pos >= p.seq) return;
-  const uint32_t t0 = split * p.split_len;
-  if (t0 > pos) return;  // dead split: writes nothing
-  const uint32_t n = min(p.split_len, pos + 1 - t0);
-  const uint32_t G = EXACT_G ? (uint32_t)GMAX : p.q_heads / p.kv_heads;
-  const uint32_t head = HEAD > 0 ? (uint32_t)HEAD : p.head;
-  const uint32_t LP = head / CH;
-  uint32_t lg_p2 = 1;
-  while ((1u << lg_p2) < LP) ++lg_p2;
-  constexpr uint32_t P2C = HEAD > 0 ? ceil_pow2(HEAD / CH) : 0;
-  const uint32_t P2 = HEAD > 0 ? P2C : (1u << lg_p2);
-  if (HEAD > 0) lg_p2 = __builtin_ctz(P2C > 0 ? P2C : 2);
-  const uint32_t lg_pw = 6 - lg_p2;
-  const uint32_t PW = 1u << lg_pw;
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t sub = lane & (P2 - 1), slot = lane / P2;
-  const bool active = sub < LP;
-  const uint32_t round = AMMON_WAVES * PW;
-  const uint32_t chunk = R * round;
-  using C = Chunk<KV, CH>;
-  using QC = Chunk<float, (CH >= 4 ? 4 : CH)>;
-  constexpr int QCH = CH >= 4 ? 4 : CH;
-
-  // Buffer resources over this split's valid positions: inactive lanes and
-  // positions past the split read zero through an out-of-range offset.
-  const uint32_t es = (uint32_t)sizeof(KV);
-  const __amdgpu_buffer_rsrc_t kres =
-      make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  const __amdgpu_buffer_rsrc_t vres =
-      make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
-  // per weight (results below 2^-126 flush to zero, far below fp32
-  // resolution of the sums).  The running maxima are kept in base-2 units
-  // and converted back (x ln 2) when the partial is written.
-  const float scale2 = 1.4426950408889634f / sqrtf((float)head);
-
-  using VT = typename C::V;
-  auto load_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t t = c0 + r * round + wave * PW + slot;
-      const uint32_t off = (t < n && active) ? (t * head + sub * CH) * es : AMMON_OOB;
-      kr[r] = C::load_buf(kres, off);
-      vr[r] = C::load_buf(vres, off);
-    }
-  };
-  // K and V of the first two chunks are requested before q is read.
-  VT kA[R], vA[R], kB[R], vB[R];
-  load_chunk(0, kA, vA);
-  load_chunk(chunk, kB, vB);
-
-  float qr[GMAX][CH];
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    const bool ok = (uint32_t)j < G && active;
-    const float *qp = p.q + (size_t)(g * G + (ok ? j : 0)) * head + sub * CH;
-#pragma unroll
-    for (int c = 0; c < CH; c += QCH) {
-      float f[QCH];
-      QC::widen(ok ? QC::load(qp + c) : QC::zero(), f);
-#pragma unroll
-      for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
-    }
-  }
-
-  float acc[GMAX][CH];
-  float m_run[GMAX], l_run[GMAX];
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) acc[j][c] = 0.f;
-  }
-
-  auto compute_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
-    // scores of this slot's R positions (-inf past the split)
-    float sc[R][GMAX];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t t = c0 + r * round + wave * PW + slot;
-      float kf[CH];
-      C::widen(kr[r], kf);
-#pragma unroll
-      for (int j = 0; j < GMAX; ++j) {
-        float d = 0.f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) d += qr[j][c] * kf[c];
-        if constexpr (HEAD > 0)
-          d = group_sum_c<P2C>(d);
-        else
-          d = group_sum(d, P2);
-        // score (reference src/kernels.rs:298: dot / sqrt(head)) in base-2
-        // units: d * log2(e) / sqrt(head)
-        sc[r][j] = t < n ? d * scale2 : -INFINITY;
-      }
-    }
-    // online softmax update of the slot's state
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j) {
-      if (!EXACT_G && (uint32_t)j >= G) continue;
-      float mc = m_run[j];
-#pragma unroll
-      for (int r = 0; r < R; ++r) mc = fmaxf(mc, sc[r][j]);
-      if (mc == -INFINITY) continue;  // nothing seen yet
-      const float a = __builtin_amdgcn_exp2f(m_run[j] - mc);
-      float l = l_run[j] * a;
-#pragma unroll
-      for (int c = 0; c < CH; ++c) acc[j][c] *= a;
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float e = __builtin_amdgcn_exp2f(sc[r][j] - mc);  // 0 for -inf scores
-        l += e;
-        float vf[CH];
-        C::widen(vr[r], vf);
-#pragma unroll
-        for (int c = 0; c < CH; ++c) acc[j][c] += e * vf[c];
-      }
-      l_run[j] = l;
-      m_run[j] = mc;
-    }
-  };
-
-  for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
-    // loads past the split read zero without touching memory, so they are
-    // issued unconditionally and the wait counts stay exact
-    compute_chunk(c0, kA, vA);
-    load_chunk(c0 + 2 * chunk, kA, vA);
-    if (c0 + chunk >= n) break;
-    compute_chunk(c0 + chunk, kB, vB);
-    load_chunk(c0 + 3 * chunk, kB, vB);
-  }
-
-  // merge the 4 * PW slots of the workgroup through LDS
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j)
-#pragma unroll
-    for (int c = 0; c < CH; ++c) s_red[threadIdx.x][j * CH + c] = acc[j][c];
-  const uint32_t slots = AMMON_WAVES * PW;
-  const uint32_t slot_id = wave * PW + slot;
-  if (sub == 0) {
-#pragma unroll
-    for (int j = 0; j < GMAX; ++j) {
-      s_m[slot_id][j] = m_run[j];
-      s_l[slot_id][j] = l_run[j];
-    }
-  }
-  __syncthreads();
-  const uint32_t slot_w = head + 2;
-  for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
-    const uint32_t j = idx / head, d = idx - j * head;
-    const uint32_t sb = d / CH, c = d % CH;  // lane sub and element (CH is a constant)
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < slots; ++s) M = fmaxf(M, s_m[s][j]);
-    float total = 0.f, L = 0.f;
-    for (uint32_t s = 0; s < slots; ++s) {
-      const float ms = s_m[s][j];
-      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      // thread of (wave s / PW, slot s % PW, sub sb)
-      const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
-      total += s_red[t][j * CH + c] * w;
-      L += s_l[s][j] * w;
-    }
-    float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
-    o[d] = total;
-    if (d == 0) {
-      o[head] = M * 0.6931471805599453f;  // back to natural-log units
-      o[head + 1] = L;
-    }
-  }
-}
+// attention.hip -- standalone split-K decode attention kernels over the
+// units in attention_impl.h: pass 1 on a (splits, kv heads) grid, pass 2 on
+// a (q heads, head / 32) grid.
+#include "attention_impl.h"
 
 #define ATT_PARTIAL(NAME, KV, CH, GMAX, HEAD, EXACT)                             \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
-    attention_partial_body<KV, CH, GMAX, HEAD, EXACT>(p);                        \
+    __shared__ float lds[att_lds_floats(GMAX, CH)];                             \
+    attention_partial_unit<KV, CH, GMAX, HEAD, EXACT>(p, blockIdx.x, blockIdx.y, lds); \
   }
 
 #define ATT_PARTIAL_G(PREFIX, KV, CH)                  \
@@ -276,59 +34,8 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_bf16_c8, uint16_t, 8)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
-// Pass 2: grid (q heads, head / 32 dim slices).  Every lane first loads, for
-// one live split, that split's max, sum and 8 of the slice's dims (one
-// round trip); the workgroup max M gives each split's weight e^{m_s - M};
-// the weighted dims and sums are reduced over the splits in LDS.  Splits
-// beyond 64 per pass are folded in by further passes over the same buffers.
-// Every workgroup of a head computes the same M and L.
-#define COMB_SPLIT_LANES 64
+
 extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine(ammon_k_attention p) {
-  __shared__ float s_acc[COMB_SPLIT_LANES][33];
-  __shared__ float s_l[COMB_SPLIT_LANES];
-  __shared__ float red[AMMON_WAVES];
-  const uint32_t h = blockIdx.x, slice = blockIdx.y;
-  const uint32_t head = p.head, slot = head + 2;
-  const uint32_t d0 = slice * 32;
-  float *out = p.out + (size_t)h * head;
-  const uint32_t pos = p.step->position;
-  if (pos >= p.seq) {
-    if (threadIdx.x < 32 && d0 + threadIdx.x < head) out[d0 + threadIdx.x] = __uint_as_float(0x7fc00000u);
-    return;
-  }
-  const uint32_t live = pos / p.split_len + 1;
-  const float *base = p.partial + (size_t)h * p.splits * slot;
-  const uint32_t sl = threadIdx.x >> 2;        // split lane, 0..63
-  const uint32_t dq = (threadIdx.x & 3) * 8;   // 8 dims of the slice
-
-  // M over all live splits
-  float m = -INFINITY;
-  for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) m = fmaxf(m, base[(size_t)s * slot + head]);
-  const float M = block_max(m, red);
-
-  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  float l = 0.f;
-  for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
-    const float *row = base + (size_t)s * slot;
-    const float w = expf(row[head] - M);
-    if ((threadIdx.x & 3) == 0) l += row[head + 1] * w;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t d = d0 + dq + k;
-      if (d < head) a[k] += row[d] * w;
-    }
-  }
-#pragma unroll
-  for (int k = 0; k < 8; ++k) s_acc[sl][dq + k] = a[k];
-  if ((threadIdx.x & 3) == 0) s_l[sl] = l;
-  __syncthreads();
-  if (threadIdx.x < 32) {
-    float total = 0.f, L = 0.f;
-    for (uint32_t s = 0; s < COMB_SPLIT_LANES; ++s) {
-      total += s_acc[s][threadIdx.x];
-      L += s_l[s];
-    }
-    const uint32_t d = d0 + threadIdx.x;
-    if (d < head) out[d] = total / L;
-  }
+  __shared__ float lds[COMB_LDS_FLOATS];
+  attention_combine_unit(p, blockIdx.x, blockIdx.y, lds);
 }

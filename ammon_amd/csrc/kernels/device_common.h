@@ -31,6 +31,32 @@ AMMON_DEV void store_elem(void *base, uint32_t dtype, size_t i, float v) {
     ((float *)base)[i] = v;
 }
 
+// Output stores at agent scope (global_store ... sc1): written through to
+// the device coherence point, so another XCD that has not cached the line
+// reads the new value without any L2 writeback.  Activations, K/V rows and
+// attention partials are stored this way; every kernel's outputs are small.
+AMMON_DEV void st_out(float *p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+AMMON_DEV void st_out(uint32_t *p, uint32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+AMMON_DEV void st_out(int32_t *p, int32_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Elements i and i + 1 (i even) of an fp32 / bf16 array as one store.
+AMMON_DEV void store_pair_out(void *base, uint32_t dtype, size_t i, float a, float b) {
+  if (dtype == AMMON_K_BF16) {
+    const uint32_t w = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
+    __hip_atomic_store((uint32_t *)((uint16_t *)base + i), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    const uint64_t w = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
+    __hip_atomic_store((uint64_t *)((float *)base + i), w, __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 AMMON_DEV float load_elem(const void *base, uint32_t dtype, size_t i) {
   if (dtype == AMMON_K_BF16) return bf16_to_f32(((const uint16_t *)base)[i]);
   return ((const float *)base)[i];

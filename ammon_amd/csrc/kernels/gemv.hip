@@ -1,386 +1,15 @@
-// gemv.hip -- bandwidth-bound batch-1 GEMV family with fused prologue and
-// epilogues (replaces the reference's Goldy matmul_into, src/kernels.rs:518-528,
-// whose definition is the serial gemv, src/kernels.rs:54-73, and the
-// surrounding rmsnorm / rope_store / cache_store / swiglu / add_into launches
-// of src/blocks.rs:219-276).
-//
-// y_i = sum_j W[i, j] x_j with W row-major [rows, n] in fp32 or bf16.
-//
-// Workgroup of 4 wave64s.  x (optionally RMS-normalised) is staged once per
-// workgroup in LDS as fp32, zero-padded to whole tiles.  Each wave owns RPW consecutive "virtual rows"
-// per row block; lane l streams the 16-byte chunks l, l+64, ... of each of
-// its rows (coalesced 1 KiB per wave per load instruction), keeping U chunk
-// loads per row in flight, multiplies them against the matching LDS slice
-// of x and reduces each row with a wave64 butterfly.  Row blocks are
-// distributed grid-stride so x is staged once per resident workgroup.  No
-// MFMA: at batch 1 the arithmetic intensity is ~1 flop/byte.
-//
-// Modes (virtual rows):
-//   PLAIN     y[r] = dot_r; with a step, y[position * d + r] (reference gemv)
-//   RESIDUAL  y[r] = residual[r] + dot_r            (y may alias residual)
-//   SWIGLU    rows interleave gate (w0) and up (w1): r = 2i -> gate row i,
-//             r = 2i+1 -> up row i; y[i] = silu(gate) * up in the reference's
-//             order (src/kernels.rs:472-475)
-//   QKV       rows run over [Wq; Wk; Wv]; (2i, 2i+1) pairs of q and k rows are
-//             rotated with the cos/sin table at step->position; q goes to y,
-//             rotated k and raw v go to the head-major caches at that position
-//             (src/kernels.rs:174-226).
-#include "device_common.h"
-
-// Work is a sequence of tiles per workgroup: tile = (row block, chunk range)
-// of RPW rows per wave x 64*U chunks.  Tiles are software-pipelined through
-// two register buffers -- the next tile's loads are in flight while the
-// current one is multiplied -- and the first tile is requested before x is
-// staged, so the prologue overlaps the first HBM round trip.
-//
-// The RMSNorm prologue sums squares with the same per-lane chunking and
-// reduction order as ammon_rmsnorm, so its normalised x matches the
-// standalone kernel bit for bit when the rows are 16-byte aligned.
-template <typename WT, int CH, int RPW, int U, int MODE>
-AMMON_DEV void gemv_body(const ammon_k_gemv &p) {
-  extern __shared__ float4 xs4[];
-  float *xs = (float *)xs4;
-  __shared__ float red[AMMON_WAVES];
-  using C = Chunk<WT, CH>;
-  using V = typename C::V;
-  const uint32_t n = p.n;
-  const uint32_t tid = threadIdx.x;
-  const uint32_t lane = tid & 63, wave = tid >> 6;
-  const uint32_t nch = n / CH;
-  const uint32_t tile_chunks = 64 * U;
-  const uint32_t tiles = (nch + tile_chunks - 1) / tile_chunks;  // per row block
-
-  // LDS layout of x in 16-byte quads.  With 8-element chunks a lane needs
-  // two quads; they are stored as two planes of 64 quads per 64 chunks, so
-  // each ds_read_b128 of a wave covers 1 KiB of consecutive addresses
-  // (conflict-free) instead of a 32-byte lane stride.
-  auto xq = [](uint32_t q) -> uint32_t {
-    if (CH == 8) return (q & ~127u) | ((q & 1u) << 6) | ((q >> 1) & 63u);
-    return q;
-  };
-  auto xi = [&](uint32_t j) -> uint32_t { return xq(j >> 2) * 4 + (j & 3u); };
-
-  // Row pointer of virtual row r0 + k; rows past the end read row 0.  The
-  // wave index is made wave-uniform so row selection stays in scalar
-  // registers, and rows start even (RPW is even), so in SWIGLU mode the
-  // gate/up choice is k's parity -- a compile-time select, never a memory
-  // read of the argument block that would have to wait behind the loads in
-  // flight.
-  const uint32_t wave_u = __builtin_amdgcn_readfirstlane(wave);
-  auto row_ptr = [&](uint32_t blk, int k) -> const WT * {
-    const uint32_t r0 = (blk * AMMON_WAVES + wave_u) * RPW;
-    const uint32_t vr = r0 + k;
-    const bool ok = vr < p.rows;
-    if (MODE == AMMON_GEMV_SWIGLU) {
-      const WT *base = (const WT *)((k & 1) ? p.w1 : p.w0);
-      return base + (size_t)(ok ? (r0 >> 1) + (k >> 1) : 0) * n;
-    } else if (MODE == AMMON_GEMV_QKV) {
-      const uint32_t r = ok ? vr : 0;
-      const WT *w0 = (const WT *)p.w0, *w1 = (const WT *)p.w1, *w2 = (const WT *)p.w2;
-      if (r < p.d) return w0 + (size_t)r * n;
-      if (r < p.d + p.kv_dim) return w1 + (size_t)(r - p.d) * n;
-      return w2 + (size_t)(r - p.d - p.kv_dim) * n;
-    }
-    return (const WT *)p.w0 + (size_t)(ok ? vr : 0) * n;
-  };
-  // Loads of tile (blk, ti) through per-row buffer resources: chunks past
-  // the row end, and every chunk of a tile past the last row block, read
-  // as zero without touching memory.  No branches, so the wait counts of
-  // the two in-flight tiles stay exact.
-  const uint32_t row_bytes = n * (uint32_t)sizeof(WT);
-  auto load_tile = [&](uint32_t blk, uint32_t ti, V (&buf)[RPW][U]) {
-    const uint32_t bytes = blk < p.row_blocks ? row_bytes : 0;
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-      const __amdgpu_buffer_rsrc_t r = make_rsrc(row_ptr(blk, k), bytes);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const uint32_t c = ti * tile_chunks + u * 64 + lane;
-        buf[k][u] = C::load_buf(r, c * (uint32_t)(CH * sizeof(WT)));
-      }
-    }
-  };
-
-  // Epilogue operands of row block blk_: QKV -> (cos, sin) of row pair k
-  // (k even) at step->position; RESIDUAL -> residual[row k].  The first
-  // block's are requested at kernel start, so a one-block workgroup does not
-  // wait on them after its last tile.
-  uint32_t pos = 0;
-  if (MODE == AMMON_GEMV_QKV) pos = p.step->position;
-  auto epi_load = [&](uint32_t blk_, float (&ea)[RPW], float (&eb)[RPW]) {
-    const uint32_t r0 = (blk_ * AMMON_WAVES + wave_u) * RPW;
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) {
-      ea[k] = 0.f;
-      eb[k] = 0.f;
-      const uint32_t vr = r0 + k;
-      if (vr >= p.rows) continue;
-      if (MODE == AMMON_GEMV_RESIDUAL) {
-        ea[k] = p.residual[vr];
-      } else if (MODE == AMMON_GEMV_QKV && (k & 1) == 0 && pos < p.seq &&
-                 vr < p.d + p.kv_dim) {
-        const uint32_t rr = vr < p.d ? vr : vr - p.d;
-        const uint32_t hd = rr % p.head;
-        const float *cs = p.table + ((size_t)pos * (p.head / 2) + hd / 2) * 2;
-        ea[k] = cs[0];
-        eb[k] = cs[1];
-      }
-    }
-  };
-  float pre_a[RPW], pre_b[RPW];
-  epi_load(blockIdx.x, pre_a, pre_b);
-
-  V bufA[RPW][U], bufB[RPW][U];
-  uint32_t blk = blockIdx.x, ti = 0;
-  // Two tiles in flight before the prologue.
-  uint32_t blk1 = blk, ti1 = ti;
-  if (++ti1 == tiles) {
-    ti1 = 0;
-    blk1 += gridDim.x;
-  }
-  load_tile(blk, ti, bufA);
-  load_tile(blk1, ti1, bufB);
-
-  // ---- stage x, optional RMSNorm prologue --------------------------------
-  // Up to XREG 16-byte chunks of x (and of the norm weight) per lane go
-  // through registers: both loads issue together, the sum of squares and the
-  // normalisation need no extra LDS pass.  Longer rows take the LDS loop.
-  constexpr int XREG = 4;
-  const bool xvec = (n & 3u) == 0 && (((uintptr_t)p.x) & 15u) == 0;
-  const bool wvec = p.norm_w == nullptr || p.norm_dtype == AMMON_K_BF16 ||
-                    (((uintptr_t)p.norm_w) & 15u) == 0;
-  if (xvec && wvec && n / 4 <= XREG * AMMON_WG) {
-    float4 xr[XREG], wr[XREG];
-    float ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < XREG; ++i) {
-      const uint32_t c = tid + i * AMMON_WG;
-      if (c < n / 4) {
-        xr[i] = ((const float4 *)p.x)[c];
-        if (p.norm_w) {
-          if (p.norm_dtype == AMMON_K_BF16) {
-            const uint2 wb = ((const uint2 *)p.norm_w)[c];
-            wr[i] = make_float4(bf16_lo(wb.x), bf16_hi(wb.x), bf16_lo(wb.y), bf16_hi(wb.y));
-          } else {
-            wr[i] = ((const float4 *)p.norm_w)[c];
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < XREG; ++i) {
-      const uint32_t c = tid + i * AMMON_WG;
-      if (c < n / 4) {
-        ss += xr[i].x * xr[i].x;
-        ss += xr[i].y * xr[i].y;
-        ss += xr[i].z * xr[i].z;
-        ss += xr[i].w * xr[i].w;
-      }
-    }
-    float s = 1.f;
-    if (p.norm_w) {
-      ss = block_sum(ss, red);
-      ss = ss / (float)n;
-      ss = ss + p.eps;
-      s = 1.0f / sqrtf(ss);
-    }
-#pragma unroll
-    for (int i = 0; i < XREG; ++i) {
-      const uint32_t c = tid + i * AMMON_WG;
-      if (c < n / 4) {
-        float4 v = xr[i];
-        if (p.norm_w)
-          v = make_float4(wr[i].x * (s * v.x), wr[i].y * (s * v.y), wr[i].z * (s * v.z),
-                          wr[i].w * (s * v.w));
-        xs4[xq(c)] = v;
-      }
-    }
-  } else {
-    float ss = 0.f;
-    if (xvec) {
-      // 16-byte loads, several in flight per lane
-#pragma unroll 4
-      for (uint32_t c = tid; c < n / 4; c += AMMON_WG) {
-        const float4 v = ((const float4 *)p.x)[c];
-        xs4[xq(c)] = v;
-        ss += v.x * v.x;
-        ss += v.y * v.y;
-        ss += v.z * v.z;
-        ss += v.w * v.w;
-      }
-    } else {
-      for (uint32_t j = tid; j < n; j += AMMON_WG) {
-        const float v = p.x[j];
-        xs[xi(j)] = v;
-        ss += v * v;
-      }
-    }
-    if (p.norm_w) {
-      ss = block_sum(ss, red);
-      ss = ss / (float)n;
-      ss = ss + p.eps;
-      const float s = 1.0f / sqrtf(ss);
-      for (uint32_t j = tid; j < n; j += AMMON_WG)
-        xs[xi(j)] = load_elem(p.norm_w, p.norm_dtype, j) * (s * xs[xi(j)]);
-    }
-  }
-  // zero padding up to whole tiles (the matching weight chunks read as 0)
-  for (uint32_t j = n + tid; j < tiles * tile_chunks * CH; j += AMMON_WG) xs[xi(j)] = 0.f;
-  __syncthreads();
-
-  // PLAIN with a step: the reference's position-strided gemv
-  // (src/kernels.rs:49-73) writes row `position` of a [seq, d] output.
-  float *yout = p.y;
-  bool write_ok = true;
-  if (MODE == AMMON_GEMV_PLAIN && p.step) {
-    const uint32_t ps = p.step->position;
-    write_ok = ps < p.seq;
-    yout = p.y + (size_t)(write_ok ? ps : 0) * p.d;
-  }
-
-  float acc[RPW];
-#pragma unroll
-  for (int k = 0; k < RPW; ++k) acc[k] = 0.f;
-
-  auto compute = [&](uint32_t ti_, V (&buf)[RPW][U]) {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const uint32_t c = ti_ * tile_chunks + u * 64 + lane;
-      float xv[CH];
-      if (CH >= 4) {
-#pragma unroll
-        for (int h = 0; h < CH / 4; ++h) {
-          const float4 v = xs4[xq(c * (CH / 4) + h)];
-          xv[4 * h] = v.x;
-          xv[4 * h + 1] = v.y;
-          xv[4 * h + 2] = v.z;
-          xv[4 * h + 3] = v.w;
-        }
-      } else {
-        xv[0] = xs[c];
-      }
-#pragma unroll
-      for (int k = 0; k < RPW; ++k) {
-        float wf[CH];
-        C::widen(buf[k][u], wf);
-        float s = acc[k];
-#pragma unroll
-        for (int e = 0; e < CH; ++e) s += wf[e] * xv[e];
-        acc[k] = s;
-      }
-    }
-  };
-
-  // Row-block epilogue (lane k handles row k / pair k).
-  auto finish = [&](uint32_t blk_) {
-    const uint32_t r0 = (blk_ * AMMON_WAVES + wave_u) * RPW;
-    float ea[RPW], eb[RPW];
-    if (blk_ == blockIdx.x) {
-#pragma unroll
-      for (int k = 0; k < RPW; ++k) {
-        ea[k] = pre_a[k];
-        eb[k] = pre_b[k];
-      }
-    } else {
-      epi_load(blk_, ea, eb);
-    }
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) acc[k] = wave_sum(acc[k]);
-    if (MODE == AMMON_GEMV_PLAIN || MODE == AMMON_GEMV_RESIDUAL) {
-#pragma unroll
-      for (int k = 0; k < RPW; ++k) {
-        const uint32_t vr = r0 + k;
-        if ((uint32_t)k == lane && vr < p.rows) {
-          if (MODE == AMMON_GEMV_RESIDUAL)
-            p.y[vr] = ea[k] + acc[k];
-          else if (write_ok)
-            yout[vr] = acc[k];
-        }
-      }
-    } else if (MODE == AMMON_GEMV_SWIGLU) {
-#pragma unroll
-      for (int k = 0; k < RPW; k += 2) {
-        const uint32_t vr = r0 + k;
-        if ((uint32_t)k == lane && vr < p.rows) {
-          const float gate = acc[k], up = acc[k + 1];
-          float v = gate * (1.0f / (1.0f + expf(-gate)));
-          v = v * up;
-          p.y[vr >> 1] = v;
-        }
-      }
-    } else {  // QKV
-#pragma clang fp contract(off)
-#pragma unroll
-      for (int k = 0; k < RPW; k += 2) {
-        const uint32_t vr = r0 + k;
-        if ((uint32_t)k != lane || vr >= p.rows) continue;
-        const float a0 = acc[k], a1 = acc[k + 1];
-        if (pos >= p.seq) {  // out-of-range position: poison q, touch no cache
-          if (vr < p.d) p.y[vr] = p.y[vr + 1] = __uint_as_float(0x7fc00000u);
-          continue;
-        }
-        if (vr < p.d + p.kv_dim) {
-          const uint32_t rr = vr < p.d ? vr : vr - p.d;
-          const uint32_t hd = rr % p.head;
-          const float fcr = ea[k], fci = eb[k];
-          const float o0 = a0 * fcr - a1 * fci;
-          const float o1 = a0 * fci + a1 * fcr;
-          if (vr < p.d) {
-            p.y[vr] = o0;
-            p.y[vr + 1] = o1;
-          } else {
-            const size_t dst = ((size_t)(rr / p.head) * p.seq + pos) * p.head + hd;
-            store_elem(p.k_cache, p.kv_dtype, dst, o0);
-            store_elem(p.k_cache, p.kv_dtype, dst + 1, o1);
-          }
-        } else {
-          const uint32_t rv = vr - p.d - p.kv_dim;
-          const size_t dst = ((size_t)(rv / p.head) * p.seq + pos) * p.head + rv % p.head;
-          store_elem(p.v_cache, p.kv_dtype, dst, a0);
-          store_elem(p.v_cache, p.kv_dtype, dst + 1, a1);
-        }
-      }
-    }
-#pragma unroll
-    for (int k = 0; k < RPW; ++k) acc[k] = 0.f;
-  };
-
-  auto next = [&](uint32_t &b, uint32_t &t) {
-    if (++t == tiles) {
-      t = 0;
-      b += gridDim.x;
-    }
-  };
-
-  // Two-stage pipeline: compute one buffer, then refill it with the tile two
-  // ahead, so the other buffer's loads stay in flight meanwhile.  Unrolled
-  // so each buffer keeps a fixed role.
-  uint32_t blk2 = blk1, ti2 = ti1;
-  next(blk2, ti2);
-  while (blk < p.row_blocks) {
-    compute(ti, bufA);
-    if (ti + 1 == tiles) finish(blk);
-    load_tile(blk2, ti2, bufA);
-    blk = blk1;
-    ti = ti1;
-    blk1 = blk2;
-    ti1 = ti2;
-    next(blk2, ti2);
-    if (blk >= p.row_blocks) break;
-    compute(ti, bufB);
-    if (ti + 1 == tiles) finish(blk);
-    load_tile(blk2, ti2, bufB);
-    blk = blk1;
-    ti = ti1;
-    blk1 = blk2;
-    ti1 = ti2;
-    next(blk2, ti2);
-  }
-}
+// gemv.hip -- standalone GEMV kernels (plain, residual, SwiGLU and QKV
+// modes, optional RMSNorm prologue) over the pass in gemv_impl.h: one launch
+// = one pass with the workgroups of the grid, x staged in dynamic LDS.
+#include "gemv_impl.h"
 
 #define GEMV_KERNEL(NAME, WT, CH, RPW, U, MODE)                                 \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemv p) { \
-    gemv_body<WT, CH, RPW, U, MODE>(p);                                        \
+    extern __shared__ float4 xs4[];                                            \
+    __shared__ float red[AMMON_WAVES];                                         \
+    GemvPass<WT, CH, RPW, U, MODE> pass;                                       \
+    pass.begin(p, blockIdx.x, gridDim.x);                                      \
+    pass.run(xs4, red);                                                        \
   }
 
 #define GEMV_MODES(PREFIX, WT, CH, RPW, U)                                    \

@@ -1,6 +1,6 @@
 // misc.hip -- elementwise SwiGLU and residual add, the greedy argmax with
 // DecodeStep feedback, and fills for synthetic weights and scratch clearing.
-#include "device_common.h"
+#include "argmax_impl.h"
 
 // hb = silu(hb) * hb2 in the reference's order (src/kernels.rs:462-476).
 extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_swiglu(ammon_k_elementwise p) {
@@ -19,43 +19,7 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_add(ammon_k_element
   p.hb[i] = p.a[i] + p.b[i];
 }
 
-// ---- argmax ------------------------------------------------------------------
-// sample_argmax (reference src/tokenizer.rs:179-189) returns the first index
-// of the maximum under a strict `>` scan from logits[0]: NaN never wins, and a
-// NaN logits[0] yields 0.  In parallel: every non-NaN element is a candidate,
-// candidates combine by (larger value, then lower index) -- a total order, so
-// the tree shape cannot change the answer -- and the NaN-logits[0] case is
-// applied at the end.  +0 and -0 compare equal, as in the scan.
-#define ARGMAX_NONE 0xffffffffu
-
-AMMON_DEV void cand_merge(float &v, uint32_t &i, float v2, uint32_t i2) {
-  if (i2 == ARGMAX_NONE) return;
-  if (i == ARGMAX_NONE || v2 > v || (!(v > v2) && i2 < i)) {
-    v = v2;
-    i = i2;
-  }
-}
-
-AMMON_DEV void block_cand_reduce(float &v, uint32_t &i) {
-  __shared__ float sv[AMMON_WG];
-  __shared__ uint32_t si[AMMON_WG];
-  sv[threadIdx.x] = v;
-  si[threadIdx.x] = i;
-  __syncthreads();
-  for (uint32_t s = AMMON_WG / 2; s > 0; s >>= 1) {
-    if (threadIdx.x < s) {
-      float a = sv[threadIdx.x];
-      uint32_t ai = si[threadIdx.x];
-      cand_merge(a, ai, sv[threadIdx.x + s], si[threadIdx.x + s]);
-      sv[threadIdx.x] = a;
-      si[threadIdx.x] = ai;
-    }
-    __syncthreads();
-  }
-  v = sv[0];
-  i = si[0];
-}
-
+// ---- argmax (candidate order in argmax_impl.h) -------------------------------
 // Pass 1: one candidate per workgroup.
 extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_partial(ammon_k_argmax p) {
   float v = 0.f;
@@ -64,7 +28,9 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_partial(ammo
     const float x = p.logits[i];
     if (x == x) cand_merge(v, idx, x, i);
   }
-  block_cand_reduce(v, idx);
+  __shared__ float sv[AMMON_WG];
+  __shared__ uint32_t si[AMMON_WG];
+  block_cand_reduce(v, idx, sv, si);
   if (threadIdx.x == 0) {
     p.cand_v[blockIdx.x] = v;
     p.cand_i[blockIdx.x] = idx;
@@ -80,7 +46,9 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_final(ammon_
   float v = 0.f;
   uint32_t idx = ARGMAX_NONE;
   for (uint32_t b = threadIdx.x; b < p.blocks; b += AMMON_WG) cand_merge(v, idx, p.cand_v[b], p.cand_i[b]);
-  block_cand_reduce(v, idx);
+  __shared__ float sv[AMMON_WG];
+  __shared__ uint32_t si[AMMON_WG];
+  block_cand_reduce(v, idx, sv, si);
   if (threadIdx.x != 0) return;
   const float first = p.logits[0];
   int32_t best = (first != first || idx == ARGMAX_NONE) ? 0 : (int32_t)idx;

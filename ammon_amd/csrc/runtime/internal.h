@@ -38,6 +38,8 @@ struct Kernels {
   hipFunction_t argmax_final = nullptr;
   hipFunction_t fill_normal = nullptr;
   hipFunction_t fill_const = nullptr;
+  // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
+  hipFunction_t token[2][kAttGroups] = {};
 };
 
 // LDS per compute unit on gfx950 (bytes); bounds resident GEMV workgroups.
@@ -52,6 +54,23 @@ constexpr uint32_t kWorkgroup = 256;
 // Resident workgroups of `f` per CU at 256 threads and `shmem` bytes of
 // dynamic LDS (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor, cached).
 uint32_t occupancy(ammon_runtime *rt, hipFunction_t f, size_t shmem);
+
+// Makes `device` current for the scope's lifetime.
+struct DeviceScope {
+  int prev = -1;
+  explicit DeviceScope(int device) {
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != device) {
+      prev = cur;
+      (void)hipSetDevice(device);
+    }
+  }
+  ~DeviceScope() {
+    if (prev >= 0) (void)hipSetDevice(prev);
+  }
+  DeviceScope(const DeviceScope &) = delete;
+  DeviceScope &operator=(const DeviceScope &) = delete;
+};
 
 ammon_status set_error(ammon_status st, const char *fmt, ...)
     __attribute__((format(printf, 2, 3)));

@@ -17,19 +17,7 @@ using namespace ammon_rt;
 
 namespace {
 
-struct DeviceGuard {
-  int prev = -1;
-  explicit DeviceGuard(int device) {
-    int cur = -1;
-    if (hipGetDevice(&cur) == hipSuccess && cur != device) {
-      prev = cur;
-      (void)hipSetDevice(device);
-    }
-  }
-  ~DeviceGuard() {
-    if (prev >= 0) (void)hipSetDevice(prev);
-  }
-};
+using DeviceGuard = ammon_rt::DeviceScope;
 
 inline uint32_t cdiv(uint64_t a, uint64_t b) { return (uint32_t)((a + b - 1) / b); }
 

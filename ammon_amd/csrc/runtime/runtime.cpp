@@ -18,7 +18,7 @@
 
 #include "internal.h"
 
-// Code objects embedded by blobs.S (one per kernels/*.hip).
+// Code objects embedded by blobs.s (one per kernels/*.hip).
 #define AMMON_BLOB(name) extern "C" const char ammon_co_##name[], ammon_co_##name##_end[];
 AMMON_BLOB(embed)
 AMMON_BLOB(norm)
@@ -26,6 +26,7 @@ AMMON_BLOB(rope)
 AMMON_BLOB(attention)
 AMMON_BLOB(gemv)
 AMMON_BLOB(misc)
+AMMON_BLOB(token)
 
 namespace ammon_rt {
 
@@ -77,9 +78,11 @@ static ammon_status load_kernels(ammon_runtime *rt) {
     const char *data;
   } blobs[] = {{"embed", ammon_co_embed}, {"norm", ammon_co_norm},
                {"rope", ammon_co_rope},   {"attention", ammon_co_attention},
-               {"gemv", ammon_co_gemv},   {"misc", ammon_co_misc}};
-  hipModule_t mods[6];
-  for (int i = 0; i < 6; ++i) {
+               {"gemv", ammon_co_gemv},   {"misc", ammon_co_misc},
+               {"token", ammon_co_token}};
+  constexpr int kModules = (int)(sizeof(blobs) / sizeof(blobs[0]));
+  hipModule_t mods[kModules];
+  for (int i = 0; i < kModules; ++i) {
     hipError_t e = hipModuleLoadData(&mods[i], blobs[i].data);
     if (e != hipSuccess)
       return set_error(AMMON_E_HIP, "load code object %s: %s", blobs[i].name, hipGetErrorString(e));
@@ -127,6 +130,12 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   R(5, "ammon_argmax_final", k.argmax_final);
   R(5, "ammon_fill_normal", k.fill_normal);
   R(5, "ammon_fill_const", k.fill_const);
+  for (int d = 0; d < 2; ++d)
+    for (int g = 0; g < kAttGroups; ++g) {
+      char name[96];
+      snprintf(name, sizeof name, "ammon_token_bf16_kv%s_g%d", dtn[d], gs[g]);
+      R(6, name, k.token[d][g]);
+    }
 #undef R
   return AMMON_OK;
 }

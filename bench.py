@@ -275,6 +275,8 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU decode for the baseline (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay launches without a graph")
+    ap.add_argument("--persistent", action="store_true",
+                    help="one persistent cooperative kernel per token")
     ap.add_argument("--split", type=int, default=0,
                     help="attention split length (0: the library's choice)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -299,7 +301,8 @@ def main():
     log(f"device {rt.info.arch.decode()} cus={rt.info.compute_units}; generating weights")
     t0 = time.time()
     model = ammon_amd.LlamaModel.synthetic(rt, c, seed=2024, std=0.02,
-                                           use_graph=not args.no_graph, split_len=args.split)
+                                           use_graph=not args.no_graph, split_len=args.split,
+                                           persistent=args.persistent)
     head = c.dim // c.n_heads
     kv_n = c.n_kv_heads * c.max_seq * head
     for l in range(c.n_layers):

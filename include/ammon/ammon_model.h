@@ -30,6 +30,9 @@ typedef struct ammon_llama_config {
   ammon_dtype kv_dtype; /* KV cache storage */
   uint32_t use_graph;   /* replay each token as a captured HIP graph */
   uint32_t split_len;   /* attention split length; 0 picks one */
+  uint32_t persistent;  /* run each token as one persistent cooperative kernel
+                           (bf16 weights, head 128, q heads per kv head in
+                           {1, 2, 4, 8}); other shapes use the launch list */
 } ammon_llama_config;
 
 typedef struct ammon_llama_weights {
@@ -91,7 +94,8 @@ ammon_status ammon_llama_tokens(ammon_llama *m, uint32_t start, uint32_t n, int3
 ammon_status ammon_llama_kv_layer(ammon_llama *m, uint32_t layer, void **key, void **value);
 ammon_status ammon_llama_stream(ammon_llama *m, ammon_stream *stream);
 ammon_status ammon_llama_logits(ammon_llama *m, float **device_logits);
-/* Number of kernel launches recorded per token (greedy step excluded). */
+/* Number of kernel launches per token (greedy step excluded): 1 when the
+ * persistent token kernel runs the model. */
 ammon_status ammon_llama_launches(ammon_llama *m, uint32_t *n);
 
 #ifdef __cplusplus

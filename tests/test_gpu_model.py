@@ -152,3 +152,42 @@ def test_model_validation(rt, c1):
     bad = oracle.LlamaConfig(**dict(json.loads(str(f["config"])), n_heads=7))
     with pytest.raises(AmmonError, match="divisible"):
         LlamaModel(rt, bad, m.weights)
+
+
+# Persistent decode-token kernel: one cooperative launch per token must give
+# the launch list's results bit for bit (same per-row and per-unit arithmetic).
+PERSISTENT_SHAPES = [  # (n_heads, n_kv_heads): q heads per kv head 4, 1, 2, 8
+    (32, 8), (8, 8), (16, 8), (32, 4)]
+
+
+@pytest.mark.parametrize("kv_dtype", [BF16, F32])
+@pytest.mark.parametrize("heads", PERSISTENT_SHAPES)
+def test_persistent_token_kernel_matches_launch_list(rt, heads, kv_dtype):
+    n_heads, n_kv = heads
+    cfg = oracle.LlamaConfig(dim=128 * n_heads, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv,
+                             hidden=1544, vocab=5003, max_seq=300, theta=500000.0,
+                             w_dtype=BF16, kv_dtype=kv_dtype)
+    ref = LlamaModel.synthetic(rt, cfg, seed=31, std=0.05)
+    for i, name in enumerate(("rms_att", "rms_ffn", "rms_final")):
+        n = cfg.dim * (cfg.n_layers if name != "rms_final" else 1)
+        rt.fill_normal(ref.weights[name], F32, n, 32, i, 1.0, 0.2)
+    rt.synchronize()
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    assert fused.launches == 1 and ref.launches == 1 + 6 * cfg.n_layers + 1
+    prompt = [7, 4093, 12, 5002, 300, 1]
+    for pos, tok in enumerate(prompt):
+        np.testing.assert_array_equal(fused.step(tok, pos), ref.step(tok, pos))
+    for l in range(cfg.n_layers):
+        for got, want in zip(fused.kv_layer(l), ref.kv_layer(l)):
+            np.testing.assert_array_equal(got, want)
+    # greedy generation past several attention splits, device loop
+    toks_f, logits_f, _ = fused.generate_tokens_device(prompt, 40)
+    toks_r, logits_r, _ = ref.generate_tokens_device(prompt, 40)
+    np.testing.assert_array_equal(toks_f, toks_r)
+    np.testing.assert_array_equal(logits_f, logits_r)
+    # decode from a late position (splits up to the cache end)
+    got = fused.decode(11, cfg.max_seq - 20, 20, read_tokens=True)
+    want = ref.decode(11, cfg.max_seq - 20, 20, read_tokens=True)
+    np.testing.assert_array_equal(got, want)
+    fused.close()
+    ref.close()
