@@ -46,7 +46,7 @@ class PersistentToken {
     const uint32_t splits = ammon_attention_splits(c.max_seq, split_len);
     // dynamic LDS: x staged for the widest GEMV input, or an attention /
     // combine / argmax unit, whichever is larger
-    const uint32_t tile = 64 * ammon_rt::kGemvTileChunks * 8;
+    const uint32_t tile = 64 * AMMON_TOKEN_GEMV_U * 8;
     auto padded = [&](uint32_t n) { return (n + tile - 1) / tile * tile; };
     const uint32_t xs = std::max(std::max(padded(c.dim), padded(c.hidden)), padded(q_dim));
     const uint32_t ach = c.kv_dtype == AMMON_BF16 ? 8 : 4;

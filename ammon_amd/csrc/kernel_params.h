@@ -126,8 +126,9 @@ typedef struct {
  * step) with grid-wide barriers between dependent phases.  Per-layer weights
  * are stacked [L, ...]; the caches are [L, kv_heads, seq, head]; sync must
  * not be shared by launches that can run at the same time. */
-#define AMMON_TOKEN_SYNC_WORDS 640 /* barrier counters (10 x 64 words)      */
 #define AMMON_TOKEN_SYNC_ERR (64 * 9) /* word set when a barrier timed out */
+#define AMMON_TOKEN_SYNC_WORDS (64 * 10)
+#define AMMON_TOKEN_GEMV_U 4 /* 16-byte chunks per lane per GEMV tile */
 typedef struct {
   const void *tok_emb;                 /* [vocab, dim] */
   const float *rms_att, *rms_ffn;      /* [L, dim] fp32 */

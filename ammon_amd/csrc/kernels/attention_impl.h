@@ -15,7 +15,7 @@
 // the reference's layout [q_heads, splits, head + 2].  Splits that start past
 // pos write nothing.
 //
-// Pass 2, one workgroup per q head: M = max m_s over live splits,
+// Pass 2, one workgroup per (q head, 32-dim slice): M = max m_s over live splits,
 // out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
 //
 // The reference uses fixed 8-position splits (src/kernels.rs:228-229); here
@@ -74,188 +74,224 @@ constexpr uint32_t att_lds_floats(int GMAX, int CH) {
   return AMMON_WG * (GMAX * CH + 1) + 2 * (AMMON_WG / 2) * GMAX;
 }
 
-// Unit (split, g) of pass 1; lds holds att_lds_floats(GMAX, CH) floats.
-// Returns without touching memory for a dead split (uniform per workgroup).
+// Unit (split, g) of pass 1, in two steps: begin() requests the K and V of
+// the split's first two chunks; run() loads q, scores, accumulates, merges
+// the slots and writes the partial (lds holds att_lds_floats(GMAX, CH)
+// floats).  A caller that starts a unit before the current position's K/V
+// row has been written passes defer_pos: that row is left out of the
+// prefetch and loaded by run().  begin() returns false for a dead split
+// (start past the position) or an out-of-range position, which write
+// nothing; the result is uniform per workgroup.
 template <typename KV, int CH, int GMAX, int HEAD, bool EXACT_G>
-AMMON_DEV void attention_partial_unit(const ammon_k_attention &p, uint32_t split, uint32_t g,
-                                      float *lds) {
-  constexpr int R = ATT_ROUNDS;
-  float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])lds;
-  float(*s_m)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1));
-  float(*s_l)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1) + (AMMON_WG / 2) * GMAX);
-
-  const uint32_t pos = p.step->position;
-  if (pos >= p.seq) return;
-  const uint32_t t0 = split * p.split_len;
-  if (t0 > pos) return;  // dead split: writes nothing
-  const uint32_t n = min(p.split_len, pos + 1 - t0);
-  const uint32_t G = EXACT_G ? (uint32_t)GMAX : p.q_heads / p.kv_heads;
-  const uint32_t head = HEAD > 0 ? (uint32_t)HEAD : p.head;
-  const uint32_t LP = head / CH;
-  uint32_t lg_p2 = 1;
-  while ((1u << lg_p2) < LP) ++lg_p2;
-  constexpr uint32_t P2C = HEAD > 0 ? ceil_pow2(HEAD / CH) : 0;
-  const uint32_t P2 = HEAD > 0 ? P2C : (1u << lg_p2);
-  if (HEAD > 0) lg_p2 = __builtin_ctz(P2C > 0 ? P2C : 2);
-  const uint32_t lg_pw = 6 - lg_p2;
-  const uint32_t PW = 1u << lg_pw;
-  const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const uint32_t sub = lane & (P2 - 1), slot = lane / P2;
-  const bool active = sub < LP;
-  const uint32_t round = AMMON_WAVES * PW;
-  const uint32_t chunk = R * round;
+struct AttnPartial {
+  static constexpr int R = ATT_ROUNDS;
+  static constexpr int QCH = CH >= 4 ? 4 : CH;
+  static constexpr uint32_t P2C = HEAD > 0 ? ceil_pow2(HEAD / CH) : 0;
   using C = Chunk<KV, CH>;
-  using QC = Chunk<float, (CH >= 4 ? 4 : CH)>;
-  constexpr int QCH = CH >= 4 ? 4 : CH;
-
-  // Buffer resources over this split's valid positions: inactive lanes and
-  // positions past the split read zero through an out-of-range offset.
-  const uint32_t es = (uint32_t)sizeof(KV);
-  const __amdgpu_buffer_rsrc_t kres =
-      make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  const __amdgpu_buffer_rsrc_t vres =
-      make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-  // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
-  // per weight (results below 2^-126 flush to zero, far below fp32
-  // resolution of the sums).  The running maxima are kept in base-2 units
-  // and converted back (x ln 2) when the partial is written.
-  const float scale2 = 1.4426950408889634f / sqrtf((float)head);
-
+  using QC = Chunk<float, QCH>;
   using VT = typename C::V;
-  auto load_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
+
+  uint32_t split, g, pos, t0, n, G, head, lg_p2, P2, lg_pw, PW, lane, wave, sub, slot, round,
+      chunk, defer_t;
+  bool active;
+  __amdgpu_buffer_rsrc_t kres, vres;
+  VT kA[R], vA[R], kB[R], vB[R];
+
+  AMMON_DEV uint32_t off_of(uint32_t t) const {
+    return (t < n && active) ? (t * head + sub * CH) * (uint32_t)sizeof(KV) : AMMON_OOB;
+  }
+  // Positions past the split read zero without touching memory, so loads
+  // are issued unconditionally and the wait counts stay exact.
+  AMMON_DEV void load_chunk(uint32_t c0, VT (&kr)[R], VT (&vr)[R], uint32_t skip) const {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint32_t t = c0 + r * round + wave * PW + slot;
-      const uint32_t off = (t < n && active) ? (t * head + sub * CH) * es : AMMON_OOB;
+      const uint32_t off = t == skip ? AMMON_OOB : off_of(t);
       kr[r] = C::load_buf(kres, off);
       vr[r] = C::load_buf(vres, off);
     }
-  };
-  // K and V of the first two chunks are requested before q is read.
-  VT kA[R], vA[R], kB[R], vB[R];
-  load_chunk(0, kA, vA);
-  load_chunk(chunk, kB, vB);
-
-  float qr[GMAX][CH];
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    const bool ok = (uint32_t)j < G && active;
-    const float *qp = p.q + (size_t)(g * G + (ok ? j : 0)) * head + sub * CH;
-#pragma unroll
-    for (int c = 0; c < CH; c += QCH) {
-      float f[QCH];
-      QC::widen(ok ? QC::load(qp + c) : QC::zero(), f);
-#pragma unroll
-      for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
-    }
   }
-
-  float acc[GMAX][CH];
-  float m_run[GMAX], l_run[GMAX];
-#pragma unroll
-  for (int j = 0; j < GMAX; ++j) {
-    m_run[j] = -INFINITY;
-    l_run[j] = 0.f;
-#pragma unroll
-    for (int c = 0; c < CH; ++c) acc[j][c] = 0.f;
-  }
-
-  auto compute_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
-    // scores of this slot's R positions (-inf past the split)
-    float sc[R][GMAX];
+  AMMON_DEV void reload_row(uint32_t c0, VT (&kr)[R], VT (&vr)[R], uint32_t t_row) const {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint32_t t = c0 + r * round + wave * PW + slot;
-      float kf[CH];
-      C::widen(kr[r], kf);
-#pragma unroll
-      for (int j = 0; j < GMAX; ++j) {
-        float d = 0.f;
-#pragma unroll
-        for (int c = 0; c < CH; ++c) d += qr[j][c] * kf[c];
-        if constexpr (HEAD > 0)
-          d = group_sum_c<P2C>(d);
-        else
-          d = group_sum(d, P2);
-        // score (reference src/kernels.rs:298: dot / sqrt(head)) in base-2
-        // units: d * log2(e) / sqrt(head)
-        sc[r][j] = t < n ? d * scale2 : -INFINITY;
+      if (t == t_row) {
+        kr[r] = C::load_buf(kres, off_of(t));
+        vr[r] = C::load_buf(vres, off_of(t));
       }
     }
-    // online softmax update of the slot's state
+  }
+
+  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_, bool defer_pos) {
+    split = split_;
+    g = g_;
+    pos = p.step->position;
+    if (pos >= p.seq) return false;
+    t0 = split * p.split_len;
+    if (t0 > pos) return false;  // dead split: writes nothing
+    n = min(p.split_len, pos + 1 - t0);
+    G = EXACT_G ? (uint32_t)GMAX : p.q_heads / p.kv_heads;
+    head = HEAD > 0 ? (uint32_t)HEAD : p.head;
+    const uint32_t LP = head / CH;
+    lg_p2 = 1;
+    while ((1u << lg_p2) < LP) ++lg_p2;
+    P2 = HEAD > 0 ? P2C : (1u << lg_p2);
+    if (HEAD > 0) lg_p2 = __builtin_ctz(P2C > 0 ? P2C : 2);
+    lg_pw = 6 - lg_p2;
+    PW = 1u << lg_pw;
+    lane = threadIdx.x & 63;
+    wave = threadIdx.x >> 6;
+    sub = lane & (P2 - 1);
+    slot = lane / P2;
+    active = sub < LP;
+    round = AMMON_WAVES * PW;
+    chunk = R * round;
+    // Buffer resources over this split's valid positions: inactive lanes and
+    // positions past the split read zero through an out-of-range offset.
+    const uint32_t es = (uint32_t)sizeof(KV);
+    kres = make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
+    vres = make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
+    defer_t = defer_pos && pos - t0 < n ? pos - t0 : 0xffffffffu;
+    load_chunk(0, kA, vA, defer_t);
+    load_chunk(chunk, kB, vB, defer_t);
+    return true;
+  }
+
+  AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
+    float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])lds;
+    float(*s_m)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1));
+    float(*s_l)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1) + (AMMON_WG / 2) * GMAX);
+    if (defer_t < 2 * chunk) {  // the deferred row sits in a prefetched chunk
+      if (defer_t < chunk)
+        reload_row(0, kA, vA, defer_t);
+      else
+        reload_row(chunk, kB, vB, defer_t);
+    }
+    // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
+    // per weight (results below 2^-126 flush to zero, far below fp32
+    // resolution of the sums).  The running maxima are kept in base-2 units
+    // and converted back (x ln 2) when the partial is written.
+    const float scale2 = 1.4426950408889634f / sqrtf((float)head);
+
+    float qr[GMAX][CH];
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) {
-      if (!EXACT_G && (uint32_t)j >= G) continue;
-      float mc = m_run[j];
+      const bool ok = (uint32_t)j < G && active;
+      const float *qp = p.q + (size_t)(g * G + (ok ? j : 0)) * head + sub * CH;
 #pragma unroll
-      for (int r = 0; r < R; ++r) mc = fmaxf(mc, sc[r][j]);
-      if (mc == -INFINITY) continue;  // nothing seen yet
-      const float a = __builtin_amdgcn_exp2f(m_run[j] - mc);
-      float l = l_run[j] * a;
+      for (int c = 0; c < CH; c += QCH) {
+        float f[QCH];
+        QC::widen(ok ? QC::load(qp + c) : QC::zero(), f);
 #pragma unroll
-      for (int c = 0; c < CH; ++c) acc[j][c] *= a;
+        for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
+      }
+    }
+
+    float acc[GMAX][CH];
+    float m_run[GMAX], l_run[GMAX];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j) {
+      m_run[j] = -INFINITY;
+      l_run[j] = 0.f;
+#pragma unroll
+      for (int c = 0; c < CH; ++c) acc[j][c] = 0.f;
+    }
+
+    auto compute_chunk = [&](uint32_t c0, VT (&kr)[R], VT (&vr)[R]) {
+      // scores of this slot's R positions (-inf past the split)
+      float sc[R][GMAX];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float e = __builtin_amdgcn_exp2f(sc[r][j] - mc);  // 0 for -inf scores
-        l += e;
-        float vf[CH];
-        C::widen(vr[r], vf);
+        const uint32_t t = c0 + r * round + wave * PW + slot;
+        float kf[CH];
+        C::widen(kr[r], kf);
 #pragma unroll
-        for (int c = 0; c < CH; ++c) acc[j][c] += e * vf[c];
+        for (int j = 0; j < GMAX; ++j) {
+          float d = 0.f;
+#pragma unroll
+          for (int c = 0; c < CH; ++c) d += qr[j][c] * kf[c];
+          if constexpr (HEAD > 0)
+            d = group_sum_c<P2C>(d);
+          else
+            d = group_sum(d, P2);
+          // score (reference src/kernels.rs:298: dot / sqrt(head)) in base-2
+          // units: d * log2(e) / sqrt(head)
+          sc[r][j] = t < n ? d * scale2 : -INFINITY;
+        }
       }
-      l_run[j] = l;
-      m_run[j] = mc;
-    }
-  };
+      // online softmax update of the slot's state
+#pragma unroll
+      for (int j = 0; j < GMAX; ++j) {
+        if (!EXACT_G && (uint32_t)j >= G) continue;
+        float mc = m_run[j];
+#pragma unroll
+        for (int r = 0; r < R; ++r) mc = fmaxf(mc, sc[r][j]);
+        if (mc == -INFINITY) continue;  // nothing seen yet
+        const float a = __builtin_amdgcn_exp2f(m_run[j] - mc);
+        float l = l_run[j] * a;
+#pragma unroll
+        for (int c = 0; c < CH; ++c) acc[j][c] *= a;
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          const float e = __builtin_amdgcn_exp2f(sc[r][j] - mc);  // 0 for -inf scores
+          l += e;
+          float vf[CH];
+          C::widen(vr[r], vf);
+#pragma unroll
+          for (int c = 0; c < CH; ++c) acc[j][c] += e * vf[c];
+        }
+        l_run[j] = l;
+        m_run[j] = mc;
+      }
+    };
 
-  for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
-    // loads past the split read zero without touching memory, so they are
-    // issued unconditionally and the wait counts stay exact
-    compute_chunk(c0, kA, vA);
-    load_chunk(c0 + 2 * chunk, kA, vA);
-    if (c0 + chunk >= n) break;
-    compute_chunk(c0 + chunk, kB, vB);
-    load_chunk(c0 + 3 * chunk, kB, vB);
-  }
+    for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
+      compute_chunk(c0, kA, vA);
+      load_chunk(c0 + 2 * chunk, kA, vA, 0xffffffffu);
+      if (c0 + chunk >= n) break;
+      compute_chunk(c0 + chunk, kB, vB);
+      load_chunk(c0 + 3 * chunk, kB, vB, 0xffffffffu);
+    }
 
-  // merge the 4 * PW slots of the workgroup through LDS
+    // merge the 4 * PW slots of the workgroup through LDS
 #pragma unroll
-  for (int j = 0; j < GMAX; ++j)
+    for (int j = 0; j < GMAX; ++j)
 #pragma unroll
-    for (int c = 0; c < CH; ++c) s_red[threadIdx.x][j * CH + c] = acc[j][c];
-  const uint32_t slots = AMMON_WAVES * PW;
-  const uint32_t slot_id = wave * PW + slot;
-  if (sub == 0) {
+      for (int c = 0; c < CH; ++c) s_red[threadIdx.x][j * CH + c] = acc[j][c];
+    const uint32_t slots = AMMON_WAVES * PW;
+    const uint32_t slot_id = wave * PW + slot;
+    if (sub == 0) {
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j) {
-      s_m[slot_id][j] = m_run[j];
-      s_l[slot_id][j] = l_run[j];
+      for (int j = 0; j < GMAX; ++j) {
+        s_m[slot_id][j] = m_run[j];
+        s_l[slot_id][j] = l_run[j];
+      }
+    }
+    __syncthreads();
+    const uint32_t slot_w = head + 2;
+    for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
+      const uint32_t j = idx / head, d = idx - j * head;
+      const uint32_t sb = d / CH, c = d % CH;  // lane sub and element (CH is a constant)
+      float M = -INFINITY;
+      for (uint32_t s = 0; s < slots; ++s) M = fmaxf(M, s_m[s][j]);
+      float total = 0.f, L = 0.f;
+      for (uint32_t s = 0; s < slots; ++s) {
+        const float ms = s_m[s][j];
+        const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
+        // thread of (wave s / PW, slot s % PW, sub sb)
+        const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
+        total += s_red[t][j * CH + c] * w;
+        L += s_l[s][j] * w;
+      }
+      float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
+      st_out(o + d, total);
+      if (d == 0) {
+        st_out(o + head, M * 0.6931471805599453f);  // back to natural-log units
+        st_out(o + head + 1, L);
+      }
     }
   }
-  __syncthreads();
-  const uint32_t slot_w = head + 2;
-  for (uint32_t idx = threadIdx.x; idx < G * head; idx += AMMON_WG) {
-    const uint32_t j = idx / head, d = idx - j * head;
-    const uint32_t sb = d / CH, c = d % CH;  // lane sub and element (CH is a constant)
-    float M = -INFINITY;
-    for (uint32_t s = 0; s < slots; ++s) M = fmaxf(M, s_m[s][j]);
-    float total = 0.f, L = 0.f;
-    for (uint32_t s = 0; s < slots; ++s) {
-      const float ms = s_m[s][j];
-      const float w = ms == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ms - M);
-      // thread of (wave s / PW, slot s % PW, sub sb)
-      const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
-      total += s_red[t][j * CH + c] * w;
-      L += s_l[s][j] * w;
-    }
-    float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
-    st_out(o + d, total);
-    if (d == 0) {
-      st_out(o + head, M * 0.6931471805599453f);  // back to natural-log units
-      st_out(o + head + 1, L);
-    }
-  }
-}
+};
 
 // Pass 2: units (q head, head / 32 dim slices).  Every lane first loads, for
 // one live split, that split's max, sum and 8 of the slice's dims (one

@@ -92,7 +92,7 @@ AMMON_DEV size_t kv_layer_elems(const ammon_k_token &P) {
 template <typename WT, typename KV, int GMAX>
 AMMON_DEV void decode_token(const ammon_k_token &P) {
   constexpr int CH = 16 / sizeof(WT);  // 16-byte weight chunks
-  constexpr int RPW = 2, U = 4;
+  constexpr int RPW = 2, U = AMMON_TOKEN_GEMV_U;
   constexpr int ACH = 16 / sizeof(KV);  // attention: 16-byte K/V chunks, head 128
   extern __shared__ float4 lds4[];
   float *lds = (float *)lds4;
@@ -163,7 +163,10 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     }
     bar.arrive();
 
-    // ---- split-K attention -----------------------------------------------
+    // ---- split-K attention ---------------------------------------------------
+    // (Requesting the first unit's K/V before this barrier, with the new row
+    // deferred, measured slower: the early loads compete with the QKV pass's
+    // last row blocks.)
     ammon_k_attention a{};
     a.q = q;
     a.k_cache = kc;
@@ -177,12 +180,17 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     a.seq = P.seq;
     a.split_len = P.split_len;
     a.splits = P.splits;
-    bar.wait();  // q and the new K/V rows written
-    for (uint32_t u = wg; u < P.kv_heads * P.splits; u += G)
-      attention_partial_unit<KV, ACH, GMAX, 128, true>(a, u % P.splits, u / P.splits, lds);
+    {
+      const uint32_t units = P.kv_heads * P.splits;
+      bar.wait();  // q and the new K/V rows written
+      for (uint32_t u = wg; u < units; u += G) {
+        AttnPartial<KV, ACH, GMAX, 128, true> unit;
+        if (unit.begin(a, u % P.splits, u / P.splits, false)) unit.run(a, lds);
+      }
+    }
     bar.arrive();
 
-    // ---- combine, output projection + residual ---------------------------
+    // ---- merge, output projection + residual --------------------------------
     {
       ammon_k_gemv g{};
       g.w0 = (const WT *)P.wo + (size_t)l * P.dim * q_dim;
