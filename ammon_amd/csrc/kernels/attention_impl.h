@@ -293,6 +293,224 @@ struct AttnPartial {
   }
 };
 
+// Pass 1 on matrix cores, for bf16 K/V and head 128 (Llama-style shapes):
+// the same unit as AttnPartial with q.k on v_mfma_f32_16x16x32_bf16.
+//
+// Chunks of 128 positions: wave w scores positions [32w, 32w + 32) of the
+// chunk as two 16x16 tiles S^T[t][h] = sum_d K[t][d] q[h][d] (A = K rows as
+// stored, B = q^T, heads as the 16 columns; heads >= G are zero).  q is
+// split into bf16 hi + lo parts (two MFMAs per 32 dims), so the products
+// keep ~16 mantissa bits of q and accumulate in fp32.  The chunk's scores go
+// to LDS; one wave per head takes the chunk max, rescales the running state
+// and turns scores into weights 2^(s - m) (one exponential per position and
+// head); then every lane accumulates 8 dims of V for its 8 positions with
+// the weights read from LDS.  All slots share the workgroup's running max,
+// so the final merge across lanes and waves is a plain sum.  The partial
+// format is the VALU unit's: (sum_t e^{s_t - m} V_t, m, l).
+template <int GMAX>
+struct AttnPartialMfma {
+  static_assert(GMAX >= 1 && GMAX <= 16, "q heads per kv head");
+  static constexpr uint32_t HEAD = 128, CHUNK = 128;
+  typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+  uint32_t split, g, pos, t0, n, lane, wave;
+  __amdgpu_buffer_rsrc_t kres, vres;
+  u32x4 kr[2][4];  // [tile][32-dim step]: K row (l % 16) of the tile, dims 32(l/16) + 8kk
+  u32x4 vr[8];     // V rows of this lane's 8 positions, dims 8(l % 16)..+7
+
+  AMMON_DEV void load_chunk(uint32_t c0) {
+#pragma unroll
+    for (int tau = 0; tau < 2; ++tau) {
+      const uint32_t t = c0 + 32 * wave + 16 * tau + (lane & 15);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const uint32_t off = t < n ? (t * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+        kr[tau][kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const uint32_t t = c0 + 32 * wave + 4 * k + (lane >> 4);
+      const uint32_t off = t < n ? (t * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
+      vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0);
+    }
+  }
+
+  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
+    split = split_;
+    g = g_;
+    pos = p.step->position;
+    if (pos >= p.seq) return false;
+    t0 = split * p.split_len;
+    if (t0 > pos) return false;  // dead split: writes nothing
+    n = min(p.split_len, pos + 1 - t0);
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    kres = make_rsrc((const uint16_t *)p.k_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
+    vres = make_rsrc((const uint16_t *)p.v_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
+    load_chunk(0);
+    return true;
+  }
+
+  // lds: att_lds_floats(GMAX, 8) floats.
+  AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
+    float(*s_red)[GMAX * 8 + 1] = (float(*)[GMAX * 8 + 1])lds;      // final merge
+    float *s_s = lds + AMMON_WG * (GMAX * 8 + 1);                     // [CHUNK][GMAX]
+    float *s_scale = s_s + CHUNK * GMAX;                              // [GMAX]
+    const float scale2 = 1.4426950408889634f / sqrtf((float)HEAD);  // log2(e)/sqrt(head)
+
+    // q^T as the B operand: lane l holds head l % 16, dims 32(l/16) + 8kk..+7
+    bf16x8 qhi[4], qlo[4];
+    {
+      const uint32_t h = lane & 15;
+      const bool ok = h < GMAX;
+      const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        const float4 a = ok ? *(const float4 *)(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 b = ok ? *(const float4 *)(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        const f32x8 f = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+        // v_cvt_pk_bf16_f32 (round to nearest even); hi + lo = q to ~16 bits
+        qhi[kk] = __builtin_convertvector(f, bf16x8);
+        qlo[kk] = __builtin_convertvector(f - __builtin_convertvector(qhi[kk], f32x8), bf16x8);
+      }
+    }
+
+    float acc[GMAX][8];
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
+    // running max / sum of the heads this wave owns: h = wave + 4i
+    constexpr int HW = (GMAX + AMMON_WAVES - 1) / AMMON_WAVES;
+    float m_run[HW], l_run[HW];
+#pragma unroll
+    for (int i = 0; i < HW; ++i) {
+      m_run[i] = -INFINITY;
+      l_run[i] = 0.f;
+    }
+
+    for (uint32_t c0 = 0; c0 < n; c0 += CHUNK) {
+      // scores of this wave's two 16-position tiles
+      f32x4 st[2];
+#pragma unroll
+      for (int tau = 0; tau < 2; ++tau) {
+        f32x4 c = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, kr[tau][kk]);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], c, 0, 0, 0);
+        }
+        st[tau] = c;
+      }
+      if (c0 > 0) __syncthreads();  // previous chunk's weights consumed
+      // D layout: lane l holds S^T[4(l/16) + r][l % 16] of the tile
+      if ((lane & 15) < GMAX) {
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const uint32_t pl = 32 * wave + 16 * tau + 4 * (lane >> 4) + r;  // position in chunk
+            // score (reference src/kernels.rs:298: dot / sqrt(head)), base-2 units
+            s_s[pl * GMAX + (lane & 15)] = c0 + pl < n ? st[tau][r] * scale2 : -INFINITY;
+          }
+      }
+      __syncthreads();
+      // next chunk's K loads overlap the softmax and V accumulation
+      if (c0 + CHUNK < n) {
+#pragma unroll
+        for (int tau = 0; tau < 2; ++tau) {
+          const uint32_t t = c0 + CHUNK + 32 * wave + 16 * tau + (lane & 15);
+#pragma unroll
+          for (int kk = 0; kk < 4; ++kk) {
+            const uint32_t off = t < n ? (t * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+            kr[tau][kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
+          }
+        }
+      }
+      // one wave per head: chunk max, running rescale, weights
+#pragma unroll
+      for (int i = 0; i < HW; ++i) {
+        const uint32_t h = wave + AMMON_WAVES * i;
+        if (h >= GMAX) continue;  // wave-uniform
+        const float a0 = s_s[lane * GMAX + h], a1 = s_s[(lane + 64) * GMAX + h];
+        const float mc = wave_max(fmaxf(a0, a1));
+        const float m_new = fmaxf(m_run[i], mc);
+        // m_new is finite: every chunk holds at least one valid position
+        const float sc = __builtin_amdgcn_exp2f(m_run[i] - m_new);  // 0 on the first chunk
+        const float e0 = __builtin_amdgcn_exp2f(a0 - m_new), e1 = __builtin_amdgcn_exp2f(a1 - m_new);
+        s_s[lane * GMAX + h] = e0;
+        s_s[(lane + 64) * GMAX + h] = e1;
+        const float ls = wave_sum(e0 + e1);
+        l_run[i] = l_run[i] * sc + ls;
+        m_run[i] = m_new;
+        if (lane == 0) s_scale[h] = sc;
+      }
+      __syncthreads();
+      // V: lane l accumulates dims 8(l % 16)..+7 of positions 32w + 4k + l/16
+#pragma unroll
+      for (int j = 0; j < GMAX; ++j) {
+        const float sc = s_scale[j];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[j][e] *= sc;
+      }
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t pl = 32 * wave + 4 * k + (lane >> 4);
+        float vf[8];
+        Chunk<uint16_t, 8>::widen(vr[k], vf);
+#pragma unroll
+        for (int j = 0; j < GMAX; ++j) {
+          const float w = s_s[pl * GMAX + j];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[j][e] += w * vf[e];
+        }
+      }
+      if (c0 + CHUNK < n) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+          const uint32_t t = c0 + CHUNK + 32 * wave + 4 * k + (lane >> 4);
+          const uint32_t off = t < n ? (t * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
+          vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0);
+        }
+      }
+    }
+
+    // merge: plain sums over the 16 position slots (4 per wave) of the group
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < GMAX; ++j)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) s_red[threadIdx.x][j * 8 + e] = acc[j][e];
+    float *s_ml = s_scale + GMAX;  // [2][GMAX]: m, l per head
+#pragma unroll
+    for (int i = 0; i < HW; ++i) {
+      const uint32_t h = wave + AMMON_WAVES * i;
+      if (h < GMAX && lane == 0) {
+        s_ml[h] = m_run[i];
+        s_ml[GMAX + h] = l_run[i];
+      }
+    }
+    __syncthreads();
+    const uint32_t slot_w = HEAD + 2;
+    for (uint32_t idx = threadIdx.x; idx < GMAX * HEAD; idx += AMMON_WG) {
+      const uint32_t j = idx / HEAD, d = idx % HEAD;
+      const uint32_t sb = d / 8, e = d % 8;
+      float total = 0.f;
+#pragma unroll
+      for (uint32_t s = 0; s < 16; ++s) total += s_red[(s >> 2) * 64 + (s & 3) * 16 + sb][j * 8 + e];
+      float *o = p.partial + ((size_t)(g * GMAX + j) * p.splits + split) * slot_w;
+      st_out(o + d, total);
+      if (d == 0) {
+        st_out(o + HEAD, s_ml[j] * 0.6931471805599453f);  // back to natural-log units
+        st_out(o + HEAD + 1, s_ml[GMAX + j]);
+      }
+    }
+  }
+};
+
 // Pass 2: units (q head, head / 32 dim slices).  Every lane first loads, for
 // one live split, that split's max, sum and 8 of the slice's dims (one
 // round trip); the workgroup max M gives each split's weight e^{m_s - M};

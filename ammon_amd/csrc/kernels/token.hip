@@ -184,8 +184,13 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
       const uint32_t units = P.kv_heads * P.splits;
       bar.wait();  // q and the new K/V rows written
       for (uint32_t u = wg; u < units; u += G) {
-        AttnPartial<KV, ACH, GMAX, 128, true> unit;
-        if (unit.begin(a, u % P.splits, u / P.splits, false)) unit.run(a, lds);
+        if constexpr (sizeof(KV) == 2) {  // the standalone kernels' choice per KV type
+          AttnPartialMfma<GMAX> unit;
+          if (unit.begin(a, u % P.splits, u / P.splits)) unit.run(a, lds);
+        } else {
+          AttnPartial<KV, ACH, GMAX, 128, true> unit;
+          if (unit.begin(a, u % P.splits, u / P.splits, false)) unit.run(a, lds);
+        }
       }
     }
     bar.arrive();
