@@ -11,6 +11,7 @@
 // device greedy step (argmax + prompt forcing + DecodeStep update) so tokens
 // can be generated back to back without host round trips.
 #include <algorithm>
+#include <cstdlib>
 #include <cstring>
 #include <memory>
 
@@ -114,8 +115,14 @@ class PersistentToken {
     p.split_len = split_len;
     p.splits = splits;
     p.eps = c.eps;
-    // a barrier polls about once per microsecond: give up after ~0.2 s
+    // a barrier polls about once per microsecond: give up after ~0.2 s.
+    // AMMON_TOKEN_SPIN_LIMIT overrides it (a tiny limit lets tests exercise
+    // the timeout report without anything hanging).
     p.spin_limit = 200000;
+    if (const char *env = std::getenv("AMMON_TOKEN_SPIN_LIMIT")) {
+      const long v = std::atol(env);
+      if (v > 0) p.spin_limit = (uint32_t)std::min<long>(v, 200000);
+    }
     prompt_ = (const int32_t *)prompt.data();
     tokens_ = (int32_t *)tokens.data();
     max_tokens_ = c.max_seq;

@@ -191,3 +191,25 @@ def test_persistent_token_kernel_matches_launch_list(rt, heads, kv_dtype):
     np.testing.assert_array_equal(got, want)
     fused.close()
     ref.close()
+
+
+def test_persistent_barrier_timeout_is_reported(rt, monkeypatch):
+    # A one-poll limit on the kernel's bounded barrier wait: the waits give up
+    # at once (nothing hangs, every access stays in bounds), the kernel marks
+    # the timeout, and the host turns it into an error instead of results.
+    cfg = oracle.LlamaConfig(dim=256, n_layers=2, n_heads=2, n_kv_heads=1, hidden=512,
+                             vocab=300, max_seq=64, theta=500000.0, w_dtype=BF16, kv_dtype=BF16)
+    ref = LlamaModel.synthetic(rt, cfg, seed=5, std=0.05)
+    monkeypatch.setenv("AMMON_TOKEN_SPIN_LIMIT", "1")
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    monkeypatch.delenv("AMMON_TOKEN_SPIN_LIMIT")
+    assert fused.launches == 1
+    with pytest.raises(AmmonError, match="grid barrier timed out"):
+        for pos in range(8):  # a timeout is certain within a few tokens
+            fused.step(1, pos)
+    fused.close()
+    # a model built without the override is unaffected
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    np.testing.assert_array_equal(fused.step(3, 0), ref.step(3, 0))
+    fused.close()
+    ref.close()
