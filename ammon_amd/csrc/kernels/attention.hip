@@ -7,7 +7,7 @@
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
     __shared__ float lds[att_lds_floats(GMAX, CH)];                             \
     AttnPartial<KV, CH, GMAX, HEAD, EXACT> unit;                                \
-    if (unit.begin(p, blockIdx.x, blockIdx.y, false)) unit.run(p, lds);         \
+    if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);         \
   }
 
 #define ATT_PARTIAL_G(PREFIX, KV, CH)                  \

@@ -74,14 +74,12 @@ constexpr uint32_t att_lds_floats(int GMAX, int CH) {
   return AMMON_WG * (GMAX * CH + 1) + 2 * (AMMON_WG / 2) * GMAX;
 }
 
-// Unit (split, g) of pass 1, in two steps: begin() requests the K and V of
-// the split's first two chunks; run() loads q, scores, accumulates, merges
-// the slots and writes the partial (lds holds att_lds_floats(GMAX, CH)
-// floats).  A caller that starts a unit before the current position's K/V
-// row has been written passes defer_pos: that row is left out of the
-// prefetch and loaded by run().  begin() returns false for a dead split
-// (start past the position) or an out-of-range position, which write
-// nothing; the result is uniform per workgroup.
+// Unit (split, g) of pass 1, in two steps: begin() requests q and the K and
+// V of the split's first two chunks; run() scores, accumulates, merges the
+// slots and writes the partial (lds holds att_lds_floats(GMAX, CH) floats).
+// begin() returns false for a dead split (start past the position) or an
+// out-of-range position, which write nothing; the result is uniform per
+// workgroup.
 template <typename KV, int CH, int GMAX, int HEAD, bool EXACT_G>
 struct AttnPartial {
   static constexpr int R = ATT_ROUNDS;
@@ -92,9 +90,10 @@ struct AttnPartial {
   using VT = typename C::V;
 
   uint32_t split, g, pos, t0, n, G, head, lg_p2, P2, lg_pw, PW, lane, wave, sub, slot, round,
-      chunk, defer_t;
+      chunk;
   bool active;
   __amdgpu_buffer_rsrc_t kres, vres;
+  float qr[GMAX][CH];
   VT kA[R], vA[R], kB[R], vB[R];
 
   AMMON_DEV uint32_t off_of(uint32_t t) const {
@@ -102,27 +101,16 @@ struct AttnPartial {
   }
   // Positions past the split read zero without touching memory, so loads
   // are issued unconditionally and the wait counts stay exact.
-  AMMON_DEV void load_chunk(uint32_t c0, VT (&kr)[R], VT (&vr)[R], uint32_t skip) const {
+  AMMON_DEV void load_chunk(uint32_t c0, VT (&kr)[R], VT (&vr)[R]) const {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      const uint32_t t = c0 + r * round + wave * PW + slot;
-      const uint32_t off = t == skip ? AMMON_OOB : off_of(t);
+      const uint32_t off = off_of(c0 + r * round + wave * PW + slot);
       kr[r] = C::load_buf(kres, off);
       vr[r] = C::load_buf(vres, off);
     }
   }
-  AMMON_DEV void reload_row(uint32_t c0, VT (&kr)[R], VT (&vr)[R], uint32_t t_row) const {
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const uint32_t t = c0 + r * round + wave * PW + slot;
-      if (t == t_row) {
-        kr[r] = C::load_buf(kres, off_of(t));
-        vr[r] = C::load_buf(vres, off_of(t));
-      }
-    }
-  }
 
-  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_, bool defer_pos) {
+  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
     split = split_;
     g = g_;
     pos = p.step->position;
@@ -151,29 +139,8 @@ struct AttnPartial {
     const uint32_t es = (uint32_t)sizeof(KV);
     kres = make_rsrc((const KV *)p.k_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
     vres = make_rsrc((const KV *)p.v_cache + ((size_t)g * p.seq + t0) * head, n * head * es);
-    defer_t = defer_pos && pos - t0 < n ? pos - t0 : 0xffffffffu;
-    load_chunk(0, kA, vA, defer_t);
-    load_chunk(chunk, kB, vB, defer_t);
-    return true;
-  }
-
-  AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
-    float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])lds;
-    float(*s_m)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1));
-    float(*s_l)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1) + (AMMON_WG / 2) * GMAX);
-    if (defer_t < 2 * chunk) {  // the deferred row sits in a prefetched chunk
-      if (defer_t < chunk)
-        reload_row(0, kA, vA, defer_t);
-      else
-        reload_row(chunk, kB, vB, defer_t);
-    }
-    // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
-    // per weight (results below 2^-126 flush to zero, far below fp32
-    // resolution of the sums).  The running maxima are kept in base-2 units
-    // and converted back (x ln 2) when the partial is written.
-    const float scale2 = 1.4426950408889634f / sqrtf((float)head);
-
-    float qr[GMAX][CH];
+    // q first: loads complete in order, so the first chunk then waits only
+    // for q and that chunk's K/V
 #pragma unroll
     for (int j = 0; j < GMAX; ++j) {
       const bool ok = (uint32_t)j < G && active;
@@ -186,6 +153,20 @@ struct AttnPartial {
         for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
       }
     }
+    load_chunk(0, kA, vA);
+    load_chunk(chunk, kB, vB);
+    return true;
+  }
+
+  AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
+    float(*s_red)[GMAX * CH + 1] = (float(*)[GMAX * CH + 1])lds;
+    float(*s_m)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1));
+    float(*s_l)[GMAX] = (float(*)[GMAX])(lds + AMMON_WG * (GMAX * CH + 1) + (AMMON_WG / 2) * GMAX);
+    // Softmax in base 2: e^(s - m) = 2^(s log2e - m log2e), one v_exp_f32
+    // per weight (results below 2^-126 flush to zero, far below fp32
+    // resolution of the sums).  The running maxima are kept in base-2 units
+    // and converted back (x ln 2) when the partial is written.
+    const float scale2 = 1.4426950408889634f / sqrtf((float)head);
 
     float acc[GMAX][CH];
     float m_run[GMAX], l_run[GMAX];
@@ -247,10 +228,10 @@ struct AttnPartial {
 
     for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
       compute_chunk(c0, kA, vA);
-      load_chunk(c0 + 2 * chunk, kA, vA, 0xffffffffu);
+      load_chunk(c0 + 2 * chunk, kA, vA);
       if (c0 + chunk >= n) break;
       compute_chunk(c0 + chunk, kB, vB);
-      load_chunk(c0 + 3 * chunk, kB, vB, 0xffffffffu);
+      load_chunk(c0 + 3 * chunk, kB, vB);
     }
 
     // merge the 4 * PW slots of the workgroup through LDS
@@ -296,43 +277,48 @@ struct AttnPartial {
 // Pass 1 on matrix cores, for bf16 K/V and head 128 (Llama-style shapes):
 // the same unit as AttnPartial with q.k on v_mfma_f32_16x16x32_bf16.
 //
-// Chunks of 128 positions: wave w scores positions [32w, 32w + 32) of the
-// chunk as two 16x16 tiles S^T[t][h] = sum_d K[t][d] q[h][d] (A = K rows as
-// stored, B = q^T, heads as the 16 columns; heads >= G are zero).  q is
-// split into bf16 hi + lo parts (two MFMAs per 32 dims), so the products
-// keep ~16 mantissa bits of q and accumulate in fp32.  The chunk's scores go
-// to LDS; one wave per head takes the chunk max, rescales the running state
-// and turns scores into weights 2^(s - m) (one exponential per position and
-// head); then every lane accumulates 8 dims of V for its 8 positions with
-// the weights read from LDS.  All slots share the workgroup's running max,
-// so the final merge across lanes and waves is a plain sum.  The partial
-// format is the VALU unit's: (sum_t e^{s_t - m} V_t, m, l).
+// Chunks of 64 positions, double-buffered in registers (the next chunk's K
+// and V are in flight while one is processed, so compute on the first half
+// of a split overlaps the arrival of the second).  Wave w scores positions
+// [16w, 16w + 16) of a chunk as one 16x16 tile S^T[t][h] = sum_d K[t][d]
+// q[h][d] (A = K rows as stored, B = q^T, heads as the 16 columns; heads
+// >= G are zero).  q is split into bf16 hi + lo parts (two MFMAs per 32
+// dims), so the products keep ~16 mantissa bits of q and accumulate in
+// fp32.  The chunk's scores go to LDS; one wave per head takes the chunk
+// max, rescales the running state and turns scores into weights 2^(s - m)
+// (one exponential per position and head); then every lane accumulates 8
+// dims of V for its 4 positions of the chunk with the weights read from
+// LDS.  All slots share the workgroup's running max, so the final merge
+// across lanes and waves is a plain sum.  The partial format is the VALU
+// unit's: (sum_t e^{s_t - m} V_t, m, l).
 template <int GMAX>
 struct AttnPartialMfma {
   static_assert(GMAX >= 1 && GMAX <= 16, "q heads per kv head");
-  static constexpr uint32_t HEAD = 128, CHUNK = 128;
+  static constexpr uint32_t HEAD = 128, CHUNK = 64;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   typedef float f32x8 __attribute__((ext_vector_type(8)));
 
   uint32_t split, g, pos, t0, n, lane, wave;
   __amdgpu_buffer_rsrc_t kres, vres;
-  u32x4 kr[2][4];  // [tile][32-dim step]: K row (l % 16) of the tile, dims 32(l/16) + 8kk
-  u32x4 vr[8];     // V rows of this lane's 8 positions, dims 8(l % 16)..+7
+  // q^T (B operand): lane l holds head l % 16, dims 32(l/16) + 8kk..+7 as fp32
+  float4 qraw[4][2];
+  // per chunk buffer: K row (l % 16) of the wave's tile, dims 32(l/16) + 8kk;
+  // V rows of the lane's 4 positions 16w + 4k + l/16, dims 8(l % 16)..+7
+  u32x4 kA[4], vA[4], kB[4], vB[4];
 
-  AMMON_DEV void load_chunk(uint32_t c0) {
+  // Positions past the split read zero without touching memory, so loads
+  // are issued unconditionally and the wait counts stay exact.
+  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) const {
+    const uint32_t tk = c0 + 16 * wave + (lane & 15);
 #pragma unroll
-    for (int tau = 0; tau < 2; ++tau) {
-      const uint32_t t = c0 + 32 * wave + 16 * tau + (lane & 15);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const uint32_t off = t < n ? (t * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
-        kr[tau][kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
-      }
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t off = tk < n ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+      kr[kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
     }
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t t = c0 + 32 * wave + 4 * k + (lane >> 4);
-      const uint32_t off = t < n ? (t * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
+    for (int k = 0; k < 4; ++k) {
+      const uint32_t tv = c0 + 16 * wave + 4 * k + (lane >> 4);
+      const uint32_t off = tv < n ? (tv * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
       vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0);
     }
   }
@@ -349,7 +335,20 @@ struct AttnPartialMfma {
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     kres = make_rsrc((const uint16_t *)p.k_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
     vres = make_rsrc((const uint16_t *)p.v_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
-    load_chunk(0);
+    // q first: loads complete in order, so the first chunk's MFMAs then wait
+    // only for q and that chunk, not for the later chunk's K/V as well
+    {
+      const uint32_t h = lane & 15;
+      const bool ok = h < GMAX;
+      const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
+#pragma unroll
+      for (int kk = 0; kk < 4; ++kk) {
+        qraw[kk][0] = ok ? *(const float4 *)(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qraw[kk][1] = ok ? *(const float4 *)(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    load_chunk(0, kA, vA);
+    load_chunk(CHUNK, kB, vB);
     return true;
   }
 
@@ -358,23 +357,18 @@ struct AttnPartialMfma {
     float(*s_red)[GMAX * 8 + 1] = (float(*)[GMAX * 8 + 1])lds;      // final merge
     float *s_s = lds + AMMON_WG * (GMAX * 8 + 1);                     // [CHUNK][GMAX]
     float *s_scale = s_s + CHUNK * GMAX;                              // [GMAX]
+    float *s_ml = s_scale + GMAX;                                     // [2][GMAX]
     const float scale2 = 1.4426950408889634f / sqrtf((float)HEAD);  // log2(e)/sqrt(head)
 
-    // q^T as the B operand: lane l holds head l % 16, dims 32(l/16) + 8kk..+7
+    // q^T as bf16 hi + lo B operands
     bf16x8 qhi[4], qlo[4];
-    {
-      const uint32_t h = lane & 15;
-      const bool ok = h < GMAX;
-      const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
 #pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const float4 a = ok ? *(const float4 *)(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const float4 b = ok ? *(const float4 *)(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-        const f32x8 f = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-        // v_cvt_pk_bf16_f32 (round to nearest even); hi + lo = q to ~16 bits
-        qhi[kk] = __builtin_convertvector(f, bf16x8);
-        qlo[kk] = __builtin_convertvector(f - __builtin_convertvector(qhi[kk], f32x8), bf16x8);
-      }
+    for (int kk = 0; kk < 4; ++kk) {
+      const float4 a = qraw[kk][0], b = qraw[kk][1];
+      const f32x8 f = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+      // v_cvt_pk_bf16_f32 (round to nearest even); hi + lo = q to ~16 bits
+      qhi[kk] = __builtin_convertvector(f, bf16x8);
+      qlo[kk] = __builtin_convertvector(f - __builtin_convertvector(qhi[kk], f32x8), bf16x8);
     }
 
     float acc[GMAX][8];
@@ -391,65 +385,45 @@ struct AttnPartialMfma {
       l_run[i] = 0.f;
     }
 
-    for (uint32_t c0 = 0; c0 < n; c0 += CHUNK) {
-      // scores of this wave's two 16-position tiles
-      f32x4 st[2];
+    auto process = [&](uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
+      // scores of this wave's 16-position tile
+      f32x4 st = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int tau = 0; tau < 2; ++tau) {
-        f32x4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 a = __builtin_bit_cast(bf16x8, kr[tau][kk]);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], c, 0, 0, 0);
-          c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], c, 0, 0, 0);
-        }
-        st[tau] = c;
+      for (int kk = 0; kk < 4; ++kk) {
+        const bf16x8 a = __builtin_bit_cast(bf16x8, kr[kk]);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], st, 0, 0, 0);
+        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], st, 0, 0, 0);
       }
       if (c0 > 0) __syncthreads();  // previous chunk's weights consumed
       // D layout: lane l holds S^T[4(l/16) + r][l % 16] of the tile
       if ((lane & 15) < GMAX) {
 #pragma unroll
-        for (int tau = 0; tau < 2; ++tau)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const uint32_t pl = 32 * wave + 16 * tau + 4 * (lane >> 4) + r;  // position in chunk
-            // score (reference src/kernels.rs:298: dot / sqrt(head)), base-2 units
-            s_s[pl * GMAX + (lane & 15)] = c0 + pl < n ? st[tau][r] * scale2 : -INFINITY;
-          }
-      }
-      __syncthreads();
-      // next chunk's K loads overlap the softmax and V accumulation
-      if (c0 + CHUNK < n) {
-#pragma unroll
-        for (int tau = 0; tau < 2; ++tau) {
-          const uint32_t t = c0 + CHUNK + 32 * wave + 16 * tau + (lane & 15);
-#pragma unroll
-          for (int kk = 0; kk < 4; ++kk) {
-            const uint32_t off = t < n ? (t * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
-            kr[tau][kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
-          }
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t pl = 16 * wave + 4 * (lane >> 4) + r;  // position in chunk
+          // score (reference src/kernels.rs:298: dot / sqrt(head)), base-2 units
+          s_s[pl * GMAX + (lane & 15)] = c0 + pl < n ? st[r] * scale2 : -INFINITY;
         }
       }
+      __syncthreads();
       // one wave per head: chunk max, running rescale, weights
 #pragma unroll
       for (int i = 0; i < HW; ++i) {
         const uint32_t h = wave + AMMON_WAVES * i;
         if (h >= GMAX) continue;  // wave-uniform
-        const float a0 = s_s[lane * GMAX + h], a1 = s_s[(lane + 64) * GMAX + h];
-        const float mc = wave_max(fmaxf(a0, a1));
+        const float a0 = s_s[lane * GMAX + h];
+        const float mc = wave_max(a0);
         const float m_new = fmaxf(m_run[i], mc);
         // m_new is finite: every chunk holds at least one valid position
         const float sc = __builtin_amdgcn_exp2f(m_run[i] - m_new);  // 0 on the first chunk
-        const float e0 = __builtin_amdgcn_exp2f(a0 - m_new), e1 = __builtin_amdgcn_exp2f(a1 - m_new);
+        const float e0 = __builtin_amdgcn_exp2f(a0 - m_new);
         s_s[lane * GMAX + h] = e0;
-        s_s[(lane + 64) * GMAX + h] = e1;
-        const float ls = wave_sum(e0 + e1);
+        const float ls = wave_sum(e0);
         l_run[i] = l_run[i] * sc + ls;
         m_run[i] = m_new;
         if (lane == 0) s_scale[h] = sc;
       }
       __syncthreads();
-      // V: lane l accumulates dims 8(l % 16)..+7 of positions 32w + 4k + l/16
+      // V: lane l accumulates dims 8(l % 16)..+7 of positions 16w + 4k + l/16
 #pragma unroll
       for (int j = 0; j < GMAX; ++j) {
         const float sc = s_scale[j];
@@ -457,8 +431,8 @@ struct AttnPartialMfma {
         for (int e = 0; e < 8; ++e) acc[j][e] *= sc;
       }
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        const uint32_t pl = 32 * wave + 4 * k + (lane >> 4);
+      for (int k = 0; k < 4; ++k) {
+        const uint32_t pl = 16 * wave + 4 * k + (lane >> 4);
         float vf[8];
         Chunk<uint16_t, 8>::widen(vr[k], vf);
 #pragma unroll
@@ -468,14 +442,14 @@ struct AttnPartialMfma {
           for (int e = 0; e < 8; ++e) acc[j][e] += w * vf[e];
         }
       }
-      if (c0 + CHUNK < n) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-          const uint32_t t = c0 + CHUNK + 32 * wave + 4 * k + (lane >> 4);
-          const uint32_t off = t < n ? (t * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
-          vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0);
-        }
-      }
+    };
+
+    for (uint32_t c0 = 0; c0 < n; c0 += 2 * CHUNK) {
+      process(c0, kA, vA);
+      load_chunk(c0 + 2 * CHUNK, kA, vA);
+      if (c0 + CHUNK >= n) break;
+      process(c0 + CHUNK, kB, vB);
+      load_chunk(c0 + 3 * CHUNK, kB, vB);
     }
 
     // merge: plain sums over the 16 position slots (4 per wave) of the group
@@ -484,7 +458,6 @@ struct AttnPartialMfma {
     for (int j = 0; j < GMAX; ++j)
 #pragma unroll
       for (int e = 0; e < 8; ++e) s_red[threadIdx.x][j * 8 + e] = acc[j][e];
-    float *s_ml = s_scale + GMAX;  // [2][GMAX]: m, l per head
 #pragma unroll
     for (int i = 0; i < HW; ++i) {
       const uint32_t h = wave + AMMON_WAVES * i;

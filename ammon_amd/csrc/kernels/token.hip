@@ -164,9 +164,6 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     bar.arrive();
 
     // ---- split-K attention ---------------------------------------------------
-    // (Requesting the first unit's K/V before this barrier, with the new row
-    // deferred, measured slower: the early loads compete with the QKV pass's
-    // last row blocks.)
     ammon_k_attention a{};
     a.q = q;
     a.k_cache = kc;
@@ -189,7 +186,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
           if (unit.begin(a, u % P.splits, u / P.splits)) unit.run(a, lds);
         } else {
           AttnPartial<KV, ACH, GMAX, 128, true> unit;
-          if (unit.begin(a, u % P.splits, u / P.splits, false)) unit.run(a, lds);
+          if (unit.begin(a, u % P.splits, u / P.splits)) unit.run(a, lds);
         }
       }
     }
