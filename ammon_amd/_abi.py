@@ -135,6 +135,7 @@ SIGNATURES.update({
     "ammon_llama_stream": (_ST, [_P, ctypes.POINTER(_P)]),
     "ammon_llama_logits": (_ST, [_P, ctypes.POINTER(_P)]),
     "ammon_llama_launches": (_ST, [_P, ctypes.POINTER(_U32)]),
+    "ammon_llama_token_trace": (_ST, [_P, _P, _SZ, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
 })
 
 

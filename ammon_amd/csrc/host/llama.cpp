@@ -34,7 +34,7 @@ class PersistentToken {
   }
 
   PersistentToken(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w,
-                  const KvCache &cache, uint32_t split_len, const Tensor &logits,
+                  const KvCache &cache, uint32_t requested_split, const Tensor &logits,
                   const Tensor &step, const Tensor &prompt, const Tensor &tokens, const float *table)
       : rt_(rt) {
     ammon_runtime *raw = rt.raw();
@@ -44,7 +44,6 @@ class PersistentToken {
     f_ = raw->k.token[di][gi];
     if (!f_) throw Error(AMMON_E_HIP, "persistent token kernel not loaded");
     const uint32_t q_dim = c.n_heads * head;
-    const uint32_t splits = ammon_attention_splits(c.max_seq, split_len);
     // dynamic LDS: x staged for the widest GEMV input, or an attention /
     // combine / argmax unit, whichever is larger
     const uint32_t tile = 64 * AMMON_TOKEN_GEMV_U * 8;
@@ -57,6 +56,18 @@ class PersistentToken {
     const uint32_t occ = ammon_rt::occupancy(raw, f_, shmem_);
     if (occ == 0) throw Error(AMMON_E_HIP, "persistent token kernel does not fit on a CU");
     grid_ = (uint32_t)raw->info.compute_units * std::min(occ, 2u);
+    // attention split: the caller's, else the shortest power of two (>= 16)
+    // whose (kv head, split) units fit the grid once -- each workgroup then
+    // streams one split, four 64-position chunks in flight
+    uint32_t split_len = requested_split;
+    if (!split_len) {
+      split_len = 16;
+      while (split_len < AMMON_ATTENTION_MAX_SPLIT &&
+             ((uint64_t)c.n_kv_heads * ammon_attention_splits(c.max_seq, split_len) > grid_ ||
+              ammon_attention_splits(c.max_seq, split_len) > AMMON_ATTENTION_MAX_SPLITS))
+        split_len *= 2;
+    }
+    const uint32_t splits = ammon_attention_splits(c.max_seq, split_len);
 
     // one slice per phase and layer, each a whole number of 256-byte lines
     auto line = [](uint64_t floats) { return (uint32_t)((floats + 63) / 64 * 64); };
@@ -126,6 +137,13 @@ class PersistentToken {
     prompt_ = (const int32_t *)prompt.data();
     tokens_ = (int32_t *)tokens.data();
     max_tokens_ = c.max_seq;
+    // AMMON_TOKEN_TRACE=1: stamp every barrier (embed, 6 per layer, LM head,
+    // argmax) of each launch; token_trace() reads the latest launch's stamps
+    if (const char *env = std::getenv("AMMON_TOKEN_TRACE"); env && std::atoi(env) > 0) {
+      p.trace_slots = 6 * L + 3;
+      trace_ = Tensor::zeros(rt, Shape::vector((size_t)4 * p.trace_slots * grid_), DType::U32);
+      p.trace = (uint64_t *)trace_.data();
+    }
   }
 
   // Enqueue one token on `s`.  greedy: argmax + prompt forcing + DecodeStep
@@ -165,6 +183,19 @@ class PersistentToken {
 
   uint32_t grid() const { return grid_; }
 
+  // Barrier stamps of the latest launch (after the stream has drained):
+  // copies up to `capacity` words; slots = 0 when tracing is off.
+  void token_trace(ammon_stream s, uint64_t *host, size_t capacity, uint32_t *slots,
+                   uint32_t *workgroups) const {
+    *slots = p_.trace_slots;
+    *workgroups = grid_;
+    const size_t words = std::min(capacity, (size_t)2 * p_.trace_slots * grid_);
+    if (!p_.trace || !words) return;
+    ammon::check(ammon_memcpy(rt_.raw(), host, p_.trace, words * 8, AMMON_COPY_D2H, s),
+                 "token trace");
+    ammon::check(ammon_stream_synchronize(rt_.raw(), s), "token trace");
+  }
+
  private:
   Runtime rt_;
   hipFunction_t f_ = nullptr;
@@ -172,7 +203,7 @@ class PersistentToken {
   ammon_k_token p_ = {};
   const int32_t *prompt_ = nullptr;
   int32_t *tokens_ = nullptr;
-  Tensor x_, q_, att_, hb_, partial_, cand_v_, cand_i_, sync_;
+  Tensor x_, q_, att_, hb_, partial_, cand_v_, cand_i_, sync_, trace_;
 };
 
 class LlamaModel : public AutoregressiveModel {
@@ -193,6 +224,11 @@ class LlamaModel : public AutoregressiveModel {
   float *device_logits() const { return (float *)logits_.data(); }
   uint32_t launches() const {
     return persistent_ ? 1u : (uint32_t)token_scheme_->ir_node_count();
+  }
+  void token_trace(uint64_t *host, size_t capacity, uint32_t *slots, uint32_t *workgroups) const {
+    *slots = 0;
+    *workgroups = 0;
+    if (persistent_) persistent_->token_trace(stream_, host, capacity, slots, workgroups);
   }
   // Host logits of the most recent step() (what generate_tokens last saw).
   const std::vector<float> &last_logits() const { return host_logits_; }
@@ -294,7 +330,7 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
     check(ammon_rope_table_host(c.theta, head_, c.max_seq, table.data()), "rope table");
     rope_table_ = Tensor::from_f32(rt, Shape::vector((uint32_t)table.size()), table);
     persistent_ = std::make_unique<PersistentToken>(
-        rt, c, w, cache_, attn_.split_len_for(c.n_kv_heads), logits_, step_, prompt_, tokens_,
+        rt, c, w, cache_, c.split_len, logits_, step_, prompt_, tokens_,
         (const float *)rope_table_.data());
   }
 }
@@ -586,6 +622,12 @@ ammon_status ammon_llama_launches(ammon_llama *m, uint32_t *n) {
   AMMON_CHECK(m && n, "llama_launches: NULL argument");
   *n = m->model->launches();
   return AMMON_OK;
+}
+
+ammon_status ammon_llama_token_trace(ammon_llama *m, uint64_t *host, size_t capacity,
+                                     uint32_t *slots, uint32_t *workgroups) {
+  AMMON_CHECK(m && slots && workgroups && (host || !capacity), "llama_token_trace: NULL argument");
+  return guarded([&] { m->model->token_trace(host, capacity, slots, workgroups); });
 }
 
 }  // extern "C"

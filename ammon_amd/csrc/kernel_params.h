@@ -128,7 +128,7 @@ typedef struct {
  * not be shared by launches that can run at the same time. */
 #define AMMON_TOKEN_SYNC_ERR (64 * 9) /* word set when a barrier timed out */
 #define AMMON_TOKEN_SYNC_WORDS (64 * 10)
-#define AMMON_TOKEN_GEMV_U 4 /* 16-byte chunks per lane per GEMV tile */
+#define AMMON_TOKEN_GEMV_U 8 /* 16-byte chunks per lane per GEMV tile */
 typedef struct {
   const void *tok_emb;                 /* [vocab, dim] */
   const float *rms_att, *rms_ffn;      /* [L, dim] fp32 */
@@ -156,6 +156,11 @@ typedef struct {
   uint32_t greedy, n_prompt, max_tokens;
   uint32_t spin_limit;                 /* polls per barrier before giving up */
   float eps;
+  /* Optional barrier timestamps (s_memrealtime, 100 MHz), or NULL: for
+   * barrier b < trace_slots, trace[2 b G + wg] is when workgroup wg arrived
+   * and trace[(2 b + 1) G + wg] when its wait ended (G = gridDim.x). */
+  uint64_t *trace;
+  uint32_t trace_slots;
 } ammon_k_token;
 
 

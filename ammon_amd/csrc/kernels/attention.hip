@@ -32,17 +32,18 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
   ATT_PARTIAL(PREFIX##_g4, KV, CH, 4, 128, true)       \
   ATT_PARTIAL(PREFIX##_g8, KV, CH, 8, 128, true)
 
-// bf16 K/V: q.k on matrix cores
-#define ATT_PARTIAL_MFMA(NAME, GMAX)                                                 \
+// bf16 K/V: q.k on matrix cores, two chunk buffers (four measured no faster
+// here: one workgroup per unit already keeps a 128-position split in flight)
+#define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
     __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
-    AttnPartialMfma<GMAX> unit;                                                     \
+    AttnPartialMfma<GMAX, NBUF> unit;                                               \
     if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);                    \
   }
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1, 2)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2, 2)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4, 2)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 2)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 

@@ -277,9 +277,10 @@ struct AttnPartial {
 // Pass 1 on matrix cores, for bf16 K/V and head 128 (Llama-style shapes):
 // the same unit as AttnPartial with q.k on v_mfma_f32_16x16x32_bf16.
 //
-// Chunks of 64 positions, double-buffered in registers (the next chunk's K
-// and V are in flight while one is processed, so compute on the first half
-// of a split overlaps the arrival of the second).  Wave w scores positions
+// Chunks of 64 positions, NBUF-buffered in registers (the next NBUF - 1
+// chunks' K and V are in flight while one is processed, so compute on the
+// first chunks of a split overlaps the arrival of the rest; a split of
+// NBUF * 64 positions is requested in one go).  Wave w scores positions
 // [16w, 16w + 16) of a chunk as one 16x16 tile S^T[t][h] = sum_d K[t][d]
 // q[h][d] (A = K rows as stored, B = q^T, heads as the 16 columns; heads
 // >= G are zero).  q is split into bf16 hi + lo parts (two MFMAs per 32
@@ -291,9 +292,10 @@ struct AttnPartial {
 // LDS.  All slots share the workgroup's running max, so the final merge
 // across lanes and waves is a plain sum.  The partial format is the VALU
 // unit's: (sum_t e^{s_t - m} V_t, m, l).
-template <int GMAX>
+template <int GMAX, int NBUF = 2>
 struct AttnPartialMfma {
   static_assert(GMAX >= 1 && GMAX <= 16, "q heads per kv head");
+  static_assert(NBUF >= 1 && NBUF <= 4, "chunk buffers");
   static constexpr uint32_t HEAD = 128, CHUNK = 64;
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
   typedef float f32x8 __attribute__((ext_vector_type(8)));
@@ -304,7 +306,7 @@ struct AttnPartialMfma {
   float4 qraw[4][2];
   // per chunk buffer: K row (l % 16) of the wave's tile, dims 32(l/16) + 8kk;
   // V rows of the lane's 4 positions 16w + 4k + l/16, dims 8(l % 16)..+7
-  u32x4 kA[4], vA[4], kB[4], vB[4];
+  u32x4 kb[NBUF][4], vb[NBUF][4];
 
   // Positions past the split read zero without touching memory, so loads
   // are issued unconditionally and the wait counts stay exact.
@@ -347,8 +349,8 @@ struct AttnPartialMfma {
         qraw[kk][1] = ok ? *(const float4 *)(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
-    load_chunk(0, kA, vA);
-    load_chunk(CHUNK, kB, vB);
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b]);
     return true;
   }
 
@@ -444,12 +446,19 @@ struct AttnPartialMfma {
       }
     };
 
-    for (uint32_t c0 = 0; c0 < n; c0 += 2 * CHUNK) {
-      process(c0, kA, vA);
-      load_chunk(c0 + 2 * CHUNK, kA, vA);
-      if (c0 + CHUNK >= n) break;
-      process(c0 + CHUNK, kB, vB);
-      load_chunk(c0 + 3 * CHUNK, kB, vB);
+    // buffers keep fixed roles (unrolled); each is refilled NBUF chunks ahead
+    for (uint32_t c0 = 0; c0 < n; c0 += NBUF * CHUNK) {
+      bool more = true;
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b) {
+        const uint32_t c = c0 + b * CHUNK;
+        if (more && c < n) {
+          process(c, kb[b], vb[b]);
+          load_chunk(c + NBUF * CHUNK, kb[b], vb[b]);
+        } else {
+          more = false;
+        }
+      }
     }
 
     // merge: plain sums over the 16 position slots (4 per wave) of the group
@@ -484,13 +493,16 @@ struct AttnPartialMfma {
   }
 };
 
-// Pass 2: units (q head, head / 32 dim slices).  Every lane first loads, for
-// one live split, that split's max, sum and 8 of the slice's dims (one
-// round trip); the workgroup max M gives each split's weight e^{m_s - M};
-// the weighted dims and sums are reduced over the splits in LDS.  Splits
-// beyond 64 per pass are folded in by further passes over the same buffers.
-// Every workgroup of a head computes the same M and L.
+// Pass 2: units (q head, head / 32 dim slices).  Lane (split lane sl, dim
+// quarter) covers splits sl, sl + 64, ...; with up to COMB_ROUNDS * 64 live
+// splits it loads each split's max, sum and 8 of the slice's dims in one
+// round trip and keeps them in registers while the workgroup max M forms
+// (more splits take a second pass over the buffer).  Each split's weight is
+// e^{m_s - M}; the weighted dims and sums are reduced over the splits in
+// LDS, in the same order either way.  Every workgroup of a head computes the
+// same M and L.
 #define COMB_SPLIT_LANES 64
+#define COMB_ROUNDS 4
 // LDS floats of one combine unit: per split lane 32 dims + 1 pad, its sum,
 // and the block reduction slots.
 #define COMB_LDS_FLOATS (COMB_SPLIT_LANES * 33 + COMB_SPLIT_LANES + AMMON_WAVES)
@@ -515,21 +527,47 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
   const uint32_t sl = threadIdx.x >> 2;        // split lane, 0..63
   const uint32_t dq = (threadIdx.x & 3) * 8;   // 8 dims of the slice
 
-  // M over all live splits
-  float m = -INFINITY;
-  for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) m = fmaxf(m, base[(size_t)s * slot + head]);
-  const float M = block_max(m, red);
-
   float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   float l = 0.f;
-  for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
-    const float *row = base + (size_t)s * slot;
-    const float w = expf(row[head] - M);
-    if ((threadIdx.x & 3) == 0) l += row[head + 1] * w;
+  if (live <= COMB_ROUNDS * COMB_SPLIT_LANES) {
+    float mv[COMB_ROUNDS], lv[COMB_ROUNDS], dv[COMB_ROUNDS][8];
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-      const uint32_t d = d0 + dq + k;
-      if (d < head) a[k] += row[d] * w;
+    for (int r = 0; r < COMB_ROUNDS; ++r) {
+      const uint32_t s = sl + r * COMB_SPLIT_LANES;
+      const float *row = base + (size_t)(s < live ? s : 0) * slot;
+      mv[r] = s < live ? row[head] : -INFINITY;
+      lv[r] = row[head + 1];
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t d = d0 + dq + k;
+        dv[r][k] = d < head ? row[d] : 0.f;
+      }
+    }
+    float m = mv[0];
+#pragma unroll
+    for (int r = 1; r < COMB_ROUNDS; ++r) m = fmaxf(m, mv[r]);
+    const float M = block_max(m, red);
+#pragma unroll
+    for (int r = 0; r < COMB_ROUNDS; ++r) {
+      if (sl + r * COMB_SPLIT_LANES >= live) break;
+      const float w = expf(mv[r] - M);
+      if ((threadIdx.x & 3) == 0) l += lv[r] * w;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) a[k] += dv[r][k] * w;
+    }
+  } else {
+    float m = -INFINITY;
+    for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) m = fmaxf(m, base[(size_t)s * slot + head]);
+    const float M = block_max(m, red);
+    for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
+      const float *row = base + (size_t)s * slot;
+      const float w = expf(row[head] - M);
+      if ((threadIdx.x & 3) == 0) l += row[head + 1] * w;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        const uint32_t d = d0 + dq + k;
+        if (d < head) a[k] += row[d] * w;
+      }
     }
   }
 #pragma unroll

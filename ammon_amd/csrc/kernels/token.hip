@@ -29,6 +29,10 @@
 // its end instead of hanging (results are then invalid; the host reports
 // it).
 //
+// With a trace buffer, thread 0 of every workgroup stamps the device clock
+// when it arrives at and when it leaves each barrier (phase timing and load
+// balance without a profiler; the stamps are a few stores per barrier).
+//
 // Requires all gridDim.x workgroups to be co-resident (cooperative launch).
 #include "argmax_impl.h"
 #include "attention_impl.h"
@@ -41,6 +45,13 @@ struct GridSync {
   uint32_t nwg;
   uint32_t k;  // barriers passed by this workgroup
   uint32_t spin_limit;
+  uint64_t *trace;
+  uint32_t trace_slots;
+
+  AMMON_DEV void stamp(uint32_t half) const {
+    if (trace && k - 1 < trace_slots)
+      trace[(size_t)(2 * (k - 1) + half) * nwg + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
+  }
 
   AMMON_DEV uint32_t poll(const uint32_t *a) const {
     return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -58,6 +69,7 @@ struct GridSync {
           __hip_atomic_fetch_add(sync + 64 * (1 + grp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       if (old + 1 == per * k)
         __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      stamp(0);
     }
   }
 
@@ -76,6 +88,7 @@ struct GridSync {
           __builtin_amdgcn_s_sleep(1);
         }
       }
+      stamp(1);
     }
     __syncthreads();
   }
@@ -99,7 +112,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
   __shared__ float red[AMMON_WAVES];
 
   const uint32_t wg = blockIdx.x, G = gridDim.x;
-  GridSync bar{P.sync, G, 0, P.spin_limit};
+  GridSync bar{P.sync, G, 0, P.spin_limit, P.trace, P.trace_slots};
   const uint32_t head = P.head, q_dim = P.q_heads * head, kv_dim = P.kv_heads * head;
   const uint32_t rows_per_block = AMMON_WAVES * RPW;
   auto blocks = [&](uint32_t rows) { return (rows + rows_per_block - 1) / rows_per_block; };
@@ -182,7 +195,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
       bar.wait();  // q and the new K/V rows written
       for (uint32_t u = wg; u < units; u += G) {
         if constexpr (sizeof(KV) == 2) {  // the standalone kernels' choice per KV type
-          AttnPartialMfma<GMAX> unit;
+          AttnPartialMfma<GMAX, 4> unit;
           if (unit.begin(a, u % P.splits, u / P.splits)) unit.run(a, lds);
         } else {
           AttnPartial<KV, ACH, GMAX, 128, true> unit;
@@ -321,7 +334,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
 }
 
 #define TOKEN_KERNEL(NAME, WT, KV, GMAX)                                          \
-  extern "C" __global__ __launch_bounds__(AMMON_WG, 2) void NAME(ammon_k_token p) { \
+  extern "C" __global__ __launch_bounds__(AMMON_WG, 1) void NAME(ammon_k_token p) { \
     decode_token<WT, KV, GMAX>(p);                                              \
   }
 

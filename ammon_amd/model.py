@@ -144,6 +144,23 @@ class LlamaModel:
         call("ammon_llama_launches", self.handle, ctypes.byref(n))
         return n.value
 
+    def token_trace(self):
+        """Barrier stamps of the persistent kernel's latest token, or None
+        when tracing is off (AMMON_TOKEN_TRACE=1 at construction enables it):
+        uint64 [barriers, 2, workgroups] of 100 MHz device-clock ticks,
+        [b, 0, w] = arrival of workgroup w at barrier b, [b, 1, w] = end of
+        its wait.  Barriers: embed, 6 per layer (QKV, attention, merge, wo,
+        gate/up, down), LM head, argmax."""
+        slots, wgs = ctypes.c_uint32(), ctypes.c_uint32()
+        call("ammon_llama_token_trace", self.handle, None, 0, ctypes.byref(slots),
+             ctypes.byref(wgs))
+        if slots.value == 0:
+            return None
+        buf = np.zeros(2 * slots.value * wgs.value, dtype=np.uint64)
+        call("ammon_llama_token_trace", self.handle, buf.ctypes.data_as(ctypes.c_void_p), buf.size,
+             ctypes.byref(slots), ctypes.byref(wgs))
+        return buf.reshape(slots.value, 2, wgs.value)
+
     def synchronize(self) -> None:
         self.rt.synchronize(self.stream)
 

@@ -167,12 +167,13 @@ def test_persistent_token_kernel_matches_launch_list(rt, heads, kv_dtype):
     cfg = oracle.LlamaConfig(dim=128 * n_heads, n_layers=2, n_heads=n_heads, n_kv_heads=n_kv,
                              hidden=1544, vocab=5003, max_seq=300, theta=500000.0,
                              w_dtype=BF16, kv_dtype=kv_dtype)
-    ref = LlamaModel.synthetic(rt, cfg, seed=31, std=0.05)
+    # the same split for both, so they merge the same partials in the same order
+    ref = LlamaModel.synthetic(rt, cfg, seed=31, std=0.05, split_len=32)
     for i, name in enumerate(("rms_att", "rms_ffn", "rms_final")):
         n = cfg.dim * (cfg.n_layers if name != "rms_final" else 1)
         rt.fill_normal(ref.weights[name], F32, n, 32, i, 1.0, 0.2)
     rt.synchronize()
-    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True, split_len=32)
     assert fused.launches == 1 and ref.launches == 1 + 6 * cfg.n_layers + 1
     prompt = [7, 4093, 12, 5002, 300, 1]
     for pos, tok in enumerate(prompt):
@@ -213,3 +214,27 @@ def test_persistent_barrier_timeout_is_reported(rt, monkeypatch):
     np.testing.assert_array_equal(fused.step(3, 0), ref.step(3, 0))
     fused.close()
     ref.close()
+
+
+def test_persistent_token_trace(rt, monkeypatch):
+    # Barrier stamps: every workgroup arrives at each barrier before its wait
+    # ends, no wait ends before the last arrival, and the phases are ordered.
+    cfg = oracle.LlamaConfig(dim=256, n_layers=3, n_heads=2, n_kv_heads=1, hidden=512,
+                             vocab=300, max_seq=64, theta=500000.0, w_dtype=BF16, kv_dtype=BF16)
+    ref = LlamaModel.synthetic(rt, cfg, seed=6, std=0.05)
+    assert ref.token_trace() is None  # launch list: nothing to trace
+    monkeypatch.setenv("AMMON_TOKEN_TRACE", "1")
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    monkeypatch.delenv("AMMON_TOKEN_TRACE")
+    toks = fused.decode(5, 0, 3, read_tokens=True)  # greedy: every barrier runs
+    np.testing.assert_array_equal(toks, ref.decode(5, 0, 3, read_tokens=True))
+    t = fused.token_trace().astype(np.int64)
+    assert t.shape[0] == 6 * cfg.n_layers + 3 and t.shape[2] >= rt.info.compute_units
+    arrive, leave = t[:, 0, :], t[:, 1, :]
+    last = t.shape[0] - 1  # only workgroup 0 waits at the final barrier
+    assert (arrive > 0).all() and (leave[:last] > 0).all() and leave[last, 0] > 0
+    assert (leave[:last] >= arrive[:last].max(axis=1, keepdims=True)).all()
+    assert (arrive[1:] >= leave[:-1].min(axis=1, keepdims=True)).all()
+    fused.close()
+    ref.close()
+
