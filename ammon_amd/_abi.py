@@ -100,6 +100,13 @@ SIGNATURES = {
     "ammon_argmax_scratch_bytes": (_SZ, [_U32]),
     "ammon_argmax": (_ST, [_P, _P, _P, _U32, _P, _P]),
     "ammon_greedy_next": (_ST, [_P, _P, _P, _U32, _P, _P, _U32, _P, _P, _U32]),
+    "ammon_prefill_gemm": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P, _P]),
+    "ammon_prefill_qkv_rope_store": (_ST, [_P, _P, _P, _U32, _P, _P, _P, _DT, _U32, _U32, _U32,
+                                           _U32, _P, _P, _P, _DT, _U32, _P, _P]),
+    "ammon_prefill_gate_up_swiglu": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _P]),
+    "ammon_attention_prefill_scratch_bytes": (_SZ, [_U32, _U32, _U32, _U32, _U32]),
+    "ammon_attention_prefill": (_ST, [_P, _P, _P, _U32, _U32, _P, _P, _DT, _U32, _U32, _U32, _P,
+                                      _U32, _U32, _P, _SZ, _P]),
 }
 
 
@@ -129,6 +136,10 @@ SIGNATURES.update({
     "ammon_llama_generate_tokens_device": (_ST, [_P, _P, _U32, _U32, ctypes.c_int, _I32, _P,
                                                  ctypes.POINTER(_U32),
                                                  ctypes.POINTER(ctypes.c_double), _P]),
+    "ammon_llama_prefill": (_ST, [_P, _P, _U32, _U32, _P]),
+    "ammon_llama_generate_tokens_prefill": (_ST, [_P, _P, _U32, _U32, ctypes.c_int, _I32, _P,
+                                                  ctypes.POINTER(_U32),
+                                                  ctypes.POINTER(ctypes.c_double), _P]),
     "ammon_llama_decode": (_ST, [_P, _U32, _U32, _U32, _P]),
     "ammon_llama_tokens": (_ST, [_P, _U32, _U32, _P]),
     "ammon_llama_kv_layer": (_ST, [_P, _U32, ctypes.POINTER(_P), ctypes.POINTER(_P)]),

@@ -217,6 +217,9 @@ class LlamaModel : public AutoregressiveModel {
 
   GenerateTokenOutput generate_device(const std::vector<int32_t> &prompt, uint32_t max_new,
                                       std::optional<int32_t> stop_on, float *last_logits);
+  GenerateTokenOutput generate_prefill(const std::vector<int32_t> &prompt, uint32_t max_new,
+                                       std::optional<int32_t> stop_on, float *last_logits);
+  void prefill(const int32_t *tokens, uint32_t n, uint32_t start, float *logits);
   void decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, int32_t *tokens);
   KvLayer kv_layer(uint32_t l) const { return cache_.layer(l); }
   void read_tokens(uint32_t start, uint32_t n, int32_t *out);
@@ -236,6 +239,8 @@ class LlamaModel : public AutoregressiveModel {
  private:
   void record_token(Scheme &s);
   void ensure_decode_scheme(uint32_t n_prompt);
+  void ensure_prefill(uint32_t n);
+  const float *rope_table();
   void deposit(uint32_t token, uint32_t pos, ammon_stream stream);
 
   Runtime rt_;
@@ -258,6 +263,9 @@ class LlamaModel : public AutoregressiveModel {
   ammon_decode_step *pinned_step_ = nullptr;
   float *pinned_logits_ = nullptr;
   std::vector<float> host_logits_;
+  // prompt prefill scratch, [capacity, width] rows
+  uint32_t pf_cap_ = 0;
+  Tensor pf_ids_, pf_x_, pf_xn_, pf_q_, pf_att_, pf_hb_, pf_partial_;
 };
 
 DType dt(ammon_dtype d) { return (DType)d; }
@@ -470,6 +478,164 @@ void LlamaModel::decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, in
   }
 }
 
+const float *LlamaModel::rope_table() {
+  if (!rope_table_.data()) {
+    std::vector<float> table(ammon_rope_table_bytes(head_, c_.max_seq) / sizeof(float));
+    check(ammon_rope_table_host(c_.theta, head_, c_.max_seq, table.data()), "rope table");
+    rope_table_ = Tensor::from_f32(rt_, Shape::vector((uint32_t)table.size()), table);
+  }
+  return (const float *)rope_table_.data();
+}
+
+void LlamaModel::ensure_prefill(uint32_t n) {
+  if (n <= pf_cap_) return;
+  const uint32_t cap = std::max(n, 16u);
+  pf_ids_ = Tensor::zeros(rt_, Shape::vector(cap), DType::I32);
+  pf_x_ = Tensor::zeros(rt_, Shape::from_dims({cap, c_.dim}), DType::F32);
+  pf_xn_ = Tensor::zeros(rt_, Shape::from_dims({cap, c_.dim}), DType::F32);
+  pf_q_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
+  pf_att_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
+  pf_hb_ = Tensor::zeros(rt_, Shape::from_dims({cap, c_.hidden}), DType::F32);
+  pf_cap_ = cap;
+}
+
+// Positions start..start+n-1 through every layer at once: embed rows, then
+// per layer rmsnorm rows, QKV GEMM (RoPE + cache stores at start + t),
+// token-batched attention, wo GEMM + residual, rmsnorm rows, gate/up GEMM +
+// SwiGLU, w2 GEMM + residual; the final norm and LM head for the last row.
+void LlamaModel::prefill(const int32_t *tokens, uint32_t n, uint32_t start, float *logits) {
+  if (n == 0) throw Error(AMMON_E_VALIDATION, "prefill: no tokens");
+  if ((uint64_t)start + n > c_.max_seq)
+    throw Error(AMMON_E_VALIDATION, "prefill: start_pos + n exceeds max_seq");
+  for (uint32_t i = 0; i < n; ++i)
+    if (tokens[i] < 0 || (uint32_t)tokens[i] >= c_.vocab)
+      throw Error(AMMON_E_VALIDATION, "prefill: token " + std::to_string(tokens[i]) +
+                                          " outside the vocab");
+  ensure_prefill(n);
+  ammon_runtime *rt = rt_.raw();
+  ammon_stream st = stream_;
+  const ammon_dtype wd = c_.w_dtype, kvd = c_.kv_dtype;
+  const uint32_t ctx = start + n;
+  // split: as many units as the device holds twice, over the context
+  const uint32_t target = 2u * (uint32_t)std::max(rt->info.compute_units, 1);
+  uint32_t split = 16;
+  while (split < AMMON_ATTENTION_MAX_SPLIT &&
+         ((uint64_t)c_.n_kv_heads * n * ammon_attention_splits(ctx, split) > target ||
+          ammon_attention_splits(ctx, split) > AMMON_ATTENTION_MAX_SPLITS))
+    split *= 2;
+  // attention partials [n][q_heads][splits over ctx][head + 2], grown on demand
+  const size_t part_bytes = ammon_attention_prefill_scratch_bytes(n, c_.n_heads, head_, ctx, split);
+  if (!pf_partial_.data() || pf_partial_.nbytes() < part_bytes)
+    pf_partial_ = Tensor::zeros(rt_, Shape::vector((uint32_t)(part_bytes / 4)), DType::F32);
+  float *x = (float *)pf_x_.data(), *xn = (float *)pf_xn_.data();
+  float *q = (float *)pf_q_.data(), *att = (float *)pf_att_.data(), *hb = (float *)pf_hb_.data();
+  const float *table = rope_table();
+  deposit((uint32_t)tokens[0], start, st);
+  check(ammon_memcpy(rt, pf_ids_.data(), tokens, sizeof(int32_t) * n, AMMON_COPY_H2D, st),
+        "prefill ids");
+  check(ammon_embed_rows(rt, st, tok_emb_.data(), wd, c_.vocab, c_.dim,
+                         (const uint32_t *)pf_ids_.data(), n, x),
+        "prefill embed");
+  const ammon_decode_step *step = (const ammon_decode_step *)step_.data();
+  for (uint32_t l = 0; l < c_.n_layers; ++l) {
+    const CausalAttentionBlockWeights &aw = attn_w_[l];
+    const SwiGluBlockWeights &fw = ffn_w_[l];
+    KvLayer kv = cache_.layer(l);
+    check(ammon_rmsnorm(rt, st, x, aw.norm.data(), AMMON_F32, xn, n, c_.dim, c_.eps),
+          "prefill rmsnorm");
+    check(ammon_prefill_qkv_rope_store(rt, st, xn, n, aw.query.data(), aw.key.data(), aw.value.data(), wd,
+                                       c_.dim, c_.n_heads, c_.n_kv_heads, head_, q, kv.key.data(),
+                                       kv.value.data(), kvd, c_.max_seq, step, table),
+          "prefill qkv");
+    check(ammon_attention_prefill(rt, st, q, n, c_.n_heads, kv.key.data(), kv.value.data(), kvd,
+                                  c_.n_kv_heads, head_, c_.max_seq, step, ctx, split,
+                                  (float *)pf_partial_.data(), part_bytes, att),
+          "prefill attention");
+    check(ammon_prefill_gemm(rt, st, aw.output.data(), wd, c_.dim, q_dim_, att, n, x, x),
+          "prefill wo");
+    check(ammon_rmsnorm(rt, st, x, fw.norm.data(), AMMON_F32, xn, n, c_.dim, c_.eps),
+          "prefill rmsnorm");
+    check(ammon_prefill_gate_up_swiglu(rt, st, xn, n, fw.gate.data(), fw.up.data(), wd, c_.dim,
+                                       c_.hidden, hb),
+          "prefill gate/up");
+    check(ammon_prefill_gemm(rt, st, fw.down.data(), wd, c_.dim, c_.hidden, hb, n, x, x),
+          "prefill w2");
+  }
+  check(ammon_gemv_rmsnorm(rt, st, x + (size_t)(n - 1) * c_.dim, rms_final_.data(), AMMON_F32,
+                           c_.eps, wcls_.data(), wd, c_.vocab, c_.dim, (float *)logits_.data()),
+        "prefill lm head");
+  // the DecodeStep a one-by-one pass would leave: the last token at its position
+  deposit((uint32_t)tokens[n - 1], start + n - 1, st);
+  if (logits) {
+    check(ammon_memcpy(rt, logits, logits_.data(), sizeof(float) * c_.vocab, AMMON_COPY_D2H, st),
+          "prefill logits");
+  }
+  check(ammon_stream_synchronize(rt, st), "prefill");
+}
+
+GenerateTokenOutput LlamaModel::generate_prefill(const std::vector<int32_t> &prompt,
+                                                 uint32_t max_new, std::optional<int32_t> stop_on,
+                                                 float *last_logits) {
+  if (prompt.empty()) throw Error(AMMON_E_VALIDATION, "expected at least one prompt token");
+  const uint32_t limit = std::min(max_new, c_.max_seq);
+  const uint32_t steps = limit > 0 ? limit - 1 : 0;
+  const uint32_t n_prompt = (uint32_t)std::min<size_t>(prompt.size(), c_.max_seq);
+  // every step is a forced prompt token: nothing to prefill ahead of
+  if (steps < n_prompt) return generate_device(prompt, max_new, stop_on, last_logits);
+  if (!persistent_) ensure_decode_scheme(n_prompt);
+  ammon_runtime *rt = rt_.raw();
+  ammon_stream st = stream_;
+  prefill(prompt.data(), n_prompt, 0, nullptr);
+  check(ammon_memcpy(rt, prompt_.data(), prompt.data(), sizeof(int32_t) * n_prompt,
+                     AMMON_COPY_H2D, st),
+        "prompt upload");
+  // forced tokens of positions 0..n-2, as the stepped loop records them
+  if (n_prompt > 1)
+    check(ammon_memcpy(rt, tokens_.data(), prompt.data() + 1, sizeof(int32_t) * (n_prompt - 1),
+                       AMMON_COPY_H2D, st),
+          "prompt tokens");
+  // the greedy step of position n-1 on the prefilled logits
+  check(ammon_greedy_next(rt, st, (const float *)logits_.data(), c_.vocab, scratch_.data(),
+                          (const int32_t *)prompt_.data(), n_prompt,
+                          (ammon_decode_step *)step_.data(), (int32_t *)tokens_.data(), c_.max_seq),
+        "prefill greedy");
+  ammon_event e0 = nullptr, e1 = nullptr;
+  check(ammon_event_create(rt, &e0), "event");
+  check(ammon_event_create(rt, &e1), "event");
+  check(ammon_event_record(rt, e0, st), "event");
+  for (uint32_t pos = n_prompt; pos < steps; ++pos) {
+    if (persistent_)
+      persistent_->launch(st, true, n_prompt);
+    else
+      decode_scheme_->submit();
+  }
+  check(ammon_event_record(rt, e1, st), "event");
+  check(ammon_stream_synchronize(rt, st), "generate");
+  if (persistent_) persistent_->check(st);
+  float ms = 0.f;
+  const uint32_t decoded = steps - n_prompt;
+  if (decoded > 0) check(ammon_event_elapsed_ms(rt, e0, e1, &ms), "event");
+  ammon_event_destroy(rt, e0);
+  ammon_event_destroy(rt, e1);
+  std::vector<int32_t> all(steps);
+  if (steps)
+    check(ammon_memcpy(rt, all.data(), tokens_.data(), sizeof(int32_t) * steps, AMMON_COPY_D2H, st),
+          "tokens");
+  if (last_logits)
+    check(ammon_memcpy(rt, last_logits, logits_.data(), sizeof(float) * c_.vocab, AMMON_COPY_D2H,
+                       st),
+          "logits");
+  check(ammon_stream_synchronize(rt, st), "generate");
+  GenerateTokenOutput out;
+  out.prompt_tokens = prompt.size();
+  for (int32_t t : all) {
+    if (stop_on && *stop_on == t) break;
+    out.tokens.push_back(t);
+  }
+  out.tokens_per_second = (decoded > 0 && ms > 0.f) ? (double)decoded / (ms * 1e-3) : 0.0;
+  return out;
+}
+
 void LlamaModel::read_tokens(uint32_t start, uint32_t n, int32_t *out) {
   if ((uint64_t)start + n > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "tokens: range exceeds max_seq");
@@ -581,6 +747,27 @@ ammon_status ammon_llama_generate_tokens_device(ammon_llama *m, const int32_t *p
   return guarded([&] {
     std::vector<int32_t> p(prompt, prompt + n_prompt);
     auto o = m->model->generate_device(
+        p, max_new_tokens, has_stop ? std::optional<int32_t>(stop_on) : std::nullopt, last_logits);
+    fill_output(o, out_tokens, n_out, tokens_per_second);
+  });
+}
+
+ammon_status ammon_llama_prefill(ammon_llama *m, const int32_t *tokens, uint32_t n,
+                                 uint32_t start_pos, float *logits) {
+  AMMON_CHECK(m && (tokens || n == 0), "llama_prefill: NULL argument");
+  return guarded([&] { m->model->prefill(tokens, n, start_pos, logits); });
+}
+
+ammon_status ammon_llama_generate_tokens_prefill(ammon_llama *m, const int32_t *prompt,
+                                                 uint32_t n_prompt, uint32_t max_new_tokens,
+                                                 int has_stop, int32_t stop_on,
+                                                 int32_t *out_tokens, uint32_t *n_out,
+                                                 double *tokens_per_second, float *last_logits) {
+  AMMON_CHECK(m && out_tokens && n_out, "llama_generate_tokens_prefill: NULL argument");
+  AMMON_CHECK(n_prompt > 0 && prompt, "expected at least one prompt token");
+  return guarded([&] {
+    std::vector<int32_t> p(prompt, prompt + n_prompt);
+    auto o = m->model->generate_prefill(
         p, max_new_tokens, has_stop ? std::optional<int32_t>(stop_on) : std::nullopt, last_logits);
     fill_output(o, out_tokens, n_out, tokens_per_second);
   });

@@ -57,6 +57,11 @@ typedef struct {
   uint32_t kv_dim, head, seq, dtype;
 } ammon_k_cache_store;
 
+/* Attention.  A grid z dimension runs several query tokens at consecutive
+ * positions (prefill): token z reads q + z q_heads head, attends at
+ * position step->position + z, and owns partial + z q_heads splits
+ * (head + 2) and out + z q_heads head.  The kernels fold z into q, partial,
+ * out and pos_add (0 for a single token). */
 typedef struct {
   const float *q;           /* [q_heads, head] */
   const void *k_cache;      /* [kv_heads, seq, head] */
@@ -65,6 +70,7 @@ typedef struct {
   float *partial;           /* [q_heads, splits, head + 2] */
   float *out;               /* [q_heads, head] (combine) */
   uint32_t q_heads, kv_heads, head, seq, split_len, splits;
+  uint32_t pos_add;         /* added to step->position */
 } ammon_k_attention;
 
 typedef struct {
@@ -101,6 +107,22 @@ typedef struct {
   float eps;
   uint32_t kv_dim, head, seq, kv_dtype; /* QKV */
 } ammon_k_gemv;
+
+/* Prefill GEMM family: the GEMV modes over `tokens` rows of x at once
+ * (Y[t] = W X[t]), on matrix cores.  QKV rotates and stores token t at
+ * position step->position + t.  Virtual rows as for the GEMV family; a
+ * 16-row wave tile never straddles q/k/v (q_dim, kv_dim multiples of 16). */
+typedef struct {
+  const void *w0, *w1, *w2; /* row-major [*, n] matrices */
+  const float *x;           /* [tokens, n] */
+  const float *residual;    /* RESIDUAL: [tokens, d] (may equal y) */
+  float *y;                 /* [tokens, d]; QKV: q [tokens, q_dim] */
+  void *k_cache, *v_cache;  /* QKV: layer views [kv_heads, seq, head] */
+  const ammon_k_step *step; /* QKV */
+  const float *table;       /* QKV: rope cos/sin [seq, head/2, 2] */
+  uint32_t d, n, rows, tokens;
+  uint32_t kv_dim, head, seq, kv_dtype; /* QKV */
+} ammon_k_gemm;
 
 typedef struct {
   const float *logits;      /* [n] */

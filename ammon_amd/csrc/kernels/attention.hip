@@ -1,13 +1,15 @@
 // attention.hip -- standalone split-K decode attention kernels over the
 // units in attention_impl.h: pass 1 on a (splits, kv heads) grid, pass 2 on
-// a (q heads, head / 32) grid.
+// a (q heads, head / 32) grid; a z dimension runs consecutive query tokens
+// (prefill).
 #include "attention_impl.h"
 
 #define ATT_PARTIAL(NAME, KV, CH, GMAX, HEAD, EXACT)                             \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p0) { \
     __shared__ float lds[att_lds_floats(GMAX, CH)];                             \
+    const ammon_k_attention p = attention_token(p0, blockIdx.z);                \
     AttnPartial<KV, CH, GMAX, HEAD, EXACT> unit;                                \
-    if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);         \
+    if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);                \
   }
 
 #define ATT_PARTIAL_G(PREFIX, KV, CH)                  \
@@ -35,8 +37,9 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 // bf16 K/V: q.k on matrix cores, two chunk buffers (four measured no faster
 // here: one workgroup per unit already keeps a 128-position split in flight)
 #define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p) { \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p0) { \
     __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
+    const ammon_k_attention p = attention_token(p0, blockIdx.z);                    \
     AttnPartialMfma<GMAX, NBUF> unit;                                               \
     if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);                    \
   }
@@ -49,5 +52,5 @@ ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine(ammon_k_attention p) {
   __shared__ float lds[COMB_LDS_FLOATS];
-  attention_combine_unit(p, blockIdx.x, blockIdx.y, lds);
+  attention_combine_unit(attention_token(p, blockIdx.z), blockIdx.x, blockIdx.y, lds);
 }

@@ -113,7 +113,7 @@ struct AttnPartial {
   AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
     split = split_;
     g = g_;
-    pos = p.step->position;
+    pos = p.step->position + p.pos_add;
     if (pos >= p.seq) return false;
     t0 = split * p.split_len;
     if (t0 > pos) return false;  // dead split: writes nothing
@@ -328,7 +328,7 @@ struct AttnPartialMfma {
   AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
     split = split_;
     g = g_;
-    pos = p.step->position;
+    pos = p.step->position + p.pos_add;
     if (pos >= p.seq) return false;
     t0 = split * p.split_len;
     if (t0 > pos) return false;  // dead split: writes nothing
@@ -493,6 +493,18 @@ struct AttnPartialMfma {
   }
 };
 
+// Query token z of a multi-token (prefill) grid: its q, partial and output
+// slices and its position offset (identity for z = 0).
+AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t z) {
+  ammon_k_attention t = p;
+  const size_t qn = (size_t)p.q_heads * p.head;
+  t.q = p.q + z * qn;
+  t.partial = p.partial + (size_t)z * p.q_heads * p.splits * (p.head + 2);
+  if (p.out) t.out = p.out + z * qn;
+  t.pos_add = p.pos_add + z;
+  return t;
+}
+
 // Pass 2: units (q head, head / 32 dim slices).  Lane (split lane sl, dim
 // quarter) covers splits sl, sl + 64, ...; with up to COMB_ROUNDS * 64 live
 // splits it loads each split's max, sum and 8 of the slice's dims in one
@@ -516,13 +528,13 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
   const uint32_t head = p.head, slot = head + 2;
   const uint32_t d0 = slice * 32;
   float *out = p.out + (size_t)h * head;
-  const uint32_t pos = p.step->position;
+  const uint32_t pos = p.step->position + p.pos_add;
   if (pos >= p.seq) {
     if (threadIdx.x < 32 && d0 + threadIdx.x < head)
       st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));
     return;
   }
-  const uint32_t live = pos / p.split_len + 1;
+  const uint32_t live = min(pos / p.split_len + 1, p.splits);
   const float *base = p.partial + (size_t)h * p.splits * slot;
   const uint32_t sl = threadIdx.x >> 2;        // split lane, 0..63
   const uint32_t dq = (threadIdx.x & 3) * 8;   // 8 dims of the slice

@@ -1,0 +1,317 @@
+// prefill.hip -- multi-token GEMMs for prompt prefill, on matrix cores.
+//
+// The reference feeds a prompt one decode step per token
+// (src/generate.rs:62-64), so each projection is a GEMV (src/kernels.rs:
+// 518-528, serial definition :54-73) per token.  Prefill runs T consecutive
+// positions through one GEMM per projection, Y[t] = W X[t], with the decode
+// GEMV's fused epilogues: PLAIN, RESIDUAL (y = residual + W x), SWIGLU (gate
+// and up rows, silu(gate) * up as src/kernels.rs:472-475) and QKV (RoPE on
+// (2i, 2i+1) pairs of q and k rows at position step->position + t, then the
+// head-major K/V cache stores of src/kernels.rs:174-226).
+//
+// Tiling.  A workgroup owns 64 virtual rows (16 per wave) x 32 tokens (two
+// 16-token column tiles) and walks the reduction in 256-wide chunks.  On
+// each 32-wide step a wave multiplies its 16 x 32 slice of W (the A operand,
+// as stored: lane l holds row l % 16, k 8(l / 16)..+7) by the tokens' x (the
+// B operand, lane l: token l % 16, the same k) with 16x16 MFMAs; lane l then
+// holds rows 4(l / 16)..+3 of token l % 16 of the result.
+//
+//   bf16 W: v_mfma_f32_16x16x32_bf16.  x is fp32, so each x is split into
+//     three bf16 parts hi + mid + lo (each the bf16 rounding of what the
+//     previous parts left): the parts sum to x exactly, every W x part
+//     product is exact in fp32, and the three MFMAs accumulate in fp32 --
+//     fp32-grade results; only the summation order differs from the GEMV.
+//   fp32 W: v_mfma_f32_16x16x4_f32, eight per 32-wide step (lane group
+//     l / 16 supplies k 8(l / 16) + e on the e-th), exact fp32 products.
+//
+// W streams from HBM through per-wave buffer resources (rows past the
+// matrix and k past the row read as zero without touching memory), two
+// chunks in flight per wave.  x is read from L2 (it is small and every
+// workgroup of the pass reads it), one chunk ahead in registers, split /
+// packed, and staged in LDS in the B-operand order: quad (step s, column
+// tile c, part q, lane l) at ((s * 2 + c) * XQ + q) * 64 + l, so every
+// operand read is a conflict-free ds_read_b128.  Column tiles past the last
+// token are skipped.
+//
+// Launch: grid (ceil(rows / 64), ceil(tokens / 32)), 256 threads.
+#include "device_common.h"
+
+namespace {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x8 __attribute__((ext_vector_type(8)));
+
+constexpr uint32_t KC = 256;        // reduction chunk
+constexpr uint32_t S = KC / 32;     // 32-wide steps per chunk
+constexpr uint32_t NT = 2;          // 16-token column tiles per workgroup
+constexpr uint32_t TB = 16 * NT;    // tokens per workgroup
+constexpr uint32_t RB = 16 * AMMON_WAVES;  // virtual rows per workgroup
+
+// WQ: 16-byte W loads per lane per step; XQ: LDS quads per lane per (step,
+// column tile) -- three bf16 parts of 8 x values, or 8 fp32 x values.
+template <typename WT> struct GemmTraits;
+template <> struct GemmTraits<uint16_t> {
+  static constexpr int WQ = 1, XQ = 3;
+};
+template <> struct GemmTraits<float> {
+  static constexpr int WQ = 2, XQ = 2;
+};
+
+template <typename WT, int MODE>
+struct GemmTile {
+  static constexpr int WQ = GemmTraits<WT>::WQ, XQ = GemmTraits<WT>::XQ;
+  static constexpr uint32_t ES = sizeof(WT);
+
+  ammon_k_gemm p;  // by value: a reference to the kernel argument would live in scratch
+  uint32_t lane, wave, vr0, tok0, row_bytes;
+  // W source of this wave: lane row `lr` of resource r0 (or r1 for the up
+  // rows of SWIGLU)
+  __amdgpu_buffer_rsrc_t r0, r1;
+  uint32_t lr;
+  bool use_r1;
+
+  AMMON_DEV GemmTile(const ammon_k_gemm &p_) : p(p_) {
+    lane = threadIdx.x & 63;
+    wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    vr0 = blockIdx.x * RB + 16 * wave;
+    tok0 = blockIdx.y * TB;
+    row_bytes = p.n * ES;
+    lr = lane & 15;
+    use_r1 = false;
+    auto rsrc = [&](const void *base, uint32_t first, uint32_t limit, uint32_t count) {
+      const uint32_t valid = first < limit ? min(count, limit - first) : 0;
+      return make_rsrc((const WT *)base + (size_t)(valid ? first : 0) * p.n, valid * row_bytes);
+    };
+    if (MODE == AMMON_GEMV_SWIGLU) {
+      // rows 0-7 of the wave tile: gate rows i0.., rows 8-15: up rows i0..
+      const uint32_t i0 = vr0 / 2;
+      r0 = rsrc(p.w0, i0, p.d, 8);
+      r1 = rsrc(p.w1, i0, p.d, 8);
+      use_r1 = lr >= 8;
+      lr &= 7;
+    } else if (MODE == AMMON_GEMV_QKV) {
+      const uint32_t kvd = p.kv_dim;
+      if (vr0 < p.d)
+        r0 = rsrc(p.w0, vr0, p.d, 16);
+      else if (vr0 < p.d + kvd)
+        r0 = rsrc(p.w1, vr0 - p.d, kvd, 16);
+      else
+        r0 = rsrc(p.w2, vr0 - p.d - kvd, kvd, 16);
+      r1 = r0;
+    } else {
+      r0 = rsrc(p.w0, vr0, p.rows, 16);
+      r1 = r0;
+    }
+  }
+
+  // W quads of chunk `ch` (k past the row end read as zero).
+  AMMON_DEV void load_w(uint32_t ch, u32x4 (&w)[S][WQ]) const {
+#pragma unroll
+    for (uint32_t s = 0; s < S; ++s) {
+      const uint32_t k = ch * KC + 32 * s + 8 * (lane >> 4);
+      const bool ok = k < p.n;
+#pragma unroll
+      for (int q = 0; q < WQ; ++q) {
+        const uint32_t off = lr * row_bytes + (k + 4 * q) * ES;
+        if (MODE == AMMON_GEMV_SWIGLU) {
+          // both resources, each lane's other one out of range: no branch
+          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r0, ok && !use_r1 ? off : AMMON_OOB, 0, 0);
+          const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r1, ok && use_r1 ? off : AMMON_OOB, 0, 0);
+          w[s][q] = a | b;
+        } else {
+          w[s][q] = __builtin_amdgcn_raw_buffer_load_b128(r0, ok ? off : AMMON_OOB, 0, 0);
+        }
+      }
+    }
+  }
+
+  // x of chunk `ch`: unit u = tid + 256 m is (token u / 32, 8-wide k group
+  // u % 32); tokens and k past the end read as zero (no branches).
+  AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[4][2]) const {
+    const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x + (size_t)tok0 * p.n, (min(p.tokens - tok0, TB)) * p.n * 4);
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t u = threadIdx.x + AMMON_WG * m;
+      const uint32_t t = u >> 5, k = ch * KC + 8 * (u & 31);
+      const uint32_t off = k < p.n ? (t * p.n + k) * 4 : AMMON_OOB;
+      x[m][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+      x[m][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
+    }
+  }
+
+  AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
+    return ((s * NT + c) * XQ + q) * 64 + l;
+  }
+
+  // Split / pack the x chunk into LDS in B-operand order.
+  AMMON_DEV void stage(const u32x4 (&x)[4][2], u32x4 *xs) const {
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const uint32_t u = threadIdx.x + AMMON_WG * m;
+      const uint32_t t = u >> 5, kg = u & 31;
+      const uint32_t s = kg >> 2, c = t >> 4, l = (t & 15) + 16 * (kg & 3);
+      if constexpr (sizeof(WT) == 2) {
+        const f32x4 a = __builtin_bit_cast(f32x4, x[m][0]), b = __builtin_bit_cast(f32x4, x[m][1]);
+        const f32x8 f = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+        const bf16x8 hi = __builtin_convertvector(f, bf16x8);
+        const f32x8 r1 = f - __builtin_convertvector(hi, f32x8);
+        const bf16x8 mid = __builtin_convertvector(r1, bf16x8);
+        const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);
+        const bf16x8 lo = __builtin_convertvector(r2, bf16x8);
+        xs[quad(s, c, 0, l)] = __builtin_bit_cast(u32x4, hi);
+        xs[quad(s, c, 1, l)] = __builtin_bit_cast(u32x4, mid);
+        xs[quad(s, c, 2, l)] = __builtin_bit_cast(u32x4, lo);
+      } else {
+        xs[quad(s, c, 0, l)] = x[m][0];
+        xs[quad(s, c, 1, l)] = x[m][1];
+      }
+    }
+  }
+
+  AMMON_DEV void compute(const u32x4 (&w)[S][WQ], const u32x4 *xs, f32x4 (&acc)[NT]) const {
+#pragma unroll
+    for (uint32_t s = 0; s < S; ++s) {
+#pragma unroll
+      for (uint32_t c = 0; c < NT; ++c) {
+        if (tok0 + 16 * c >= p.tokens) continue;  // uniform
+        if constexpr (sizeof(WT) == 2) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, w[s][0]);
+#pragma unroll
+          for (int q = 0; q < 3; ++q) {
+            const bf16x8 b = __builtin_bit_cast(bf16x8, xs[quad(s, c, q, lane)]);
+            acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc[c], 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int q = 0; q < 2; ++q) {
+            const f32x4 a = __builtin_bit_cast(f32x4, w[s][q]);
+            const f32x4 b = __builtin_bit_cast(f32x4, xs[quad(s, c, q, lane)]);
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], b[e], acc[c], 0, 0, 0);
+          }
+        }
+      }
+    }
+  }
+
+  // Lane l holds rows 4(l / 16) + r of the wave tile, token tok0 + 16c + l % 16.
+  AMMON_DEV void epilogue(f32x4 (&acc)[NT]) const {
+    const uint32_t rq = 4 * (lane >> 4);
+#pragma unroll
+    for (uint32_t c = 0; c < NT; ++c) {
+      const uint32_t t = tok0 + 16 * c + (lane & 15);
+      if (MODE == AMMON_GEMV_SWIGLU) {
+        // gate rows sit in lanes 0-31, the matching up rows 32 lanes higher
+        float up[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(acc[c][r], 32);
+        if (lane >= 32 || t >= p.tokens) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t i = vr0 / 2 + rq + r;
+          if (i >= p.d) continue;
+          const float gate = acc[c][r];
+          float v = gate * (1.0f / (1.0f + expf(-gate)));
+          v = v * up[r];
+          p.y[(size_t)t * p.d + i] = v;
+        }
+      } else if (MODE == AMMON_GEMV_QKV) {
+#pragma clang fp contract(off)
+        if (t >= p.tokens) continue;
+        const uint32_t pos = p.step->position + t;
+        const uint32_t kvd = p.kv_dim;
+#pragma unroll
+        for (int r = 0; r < 4; r += 2) {
+          const uint32_t vr = vr0 + rq + r;
+          if (vr >= p.rows) continue;
+          const float a0 = acc[c][r], a1 = acc[c][r + 1];
+          if (pos >= p.seq) {  // out-of-range position: poison q, touch no cache
+            if (vr < p.d) {
+              p.y[(size_t)t * p.d + vr] = __uint_as_float(0x7fc00000u);
+              p.y[(size_t)t * p.d + vr + 1] = __uint_as_float(0x7fc00000u);
+            }
+            continue;
+          }
+          if (vr < p.d + kvd) {
+            const uint32_t rr = vr < p.d ? vr : vr - p.d;
+            const uint32_t hd = rr % p.head;
+            const float *cs = p.table + ((size_t)pos * (p.head / 2) + hd / 2) * 2;
+            const float fcr = cs[0], fci = cs[1];
+            const float o0 = a0 * fcr - a1 * fci;
+            const float o1 = a0 * fci + a1 * fcr;
+            if (vr < p.d) {
+              p.y[(size_t)t * p.d + vr] = o0;
+              p.y[(size_t)t * p.d + vr + 1] = o1;
+            } else {
+              store_pair_out(p.k_cache, p.kv_dtype, ((size_t)(rr / p.head) * p.seq + pos) * p.head + hd,
+                             o0, o1);
+            }
+          } else {
+            const uint32_t rv = vr - p.d - kvd;
+            store_pair_out(p.v_cache, p.kv_dtype,
+                           ((size_t)(rv / p.head) * p.seq + pos) * p.head + rv % p.head, a0, a1);
+          }
+        }
+      } else {
+        if (t >= p.tokens) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t vr = vr0 + rq + r;
+          if (vr >= p.rows) continue;
+          const size_t at = (size_t)t * p.d + vr;
+          p.y[at] = MODE == AMMON_GEMV_RESIDUAL ? p.residual[at] + acc[c][r] : acc[c][r];
+        }
+      }
+    }
+  }
+};
+
+template <typename WT, int MODE>
+AMMON_DEV void gemm(const ammon_k_gemm &p) {
+  using T = GemmTile<WT, MODE>;
+  __shared__ u32x4 xs[S * NT * T::XQ * 64];
+  T tile(p);
+  f32x4 acc[NT];
+#pragma unroll
+  for (uint32_t c = 0; c < NT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t chunks = (p.n + KC - 1) / KC;
+  u32x4 wa[S][T::WQ], wb[S][T::WQ];
+  u32x4 xr[4][2];
+  tile.load_w(0, wa);
+  tile.load_w(1, wb);
+  tile.load_x(0, xr);
+  // Two W buffers with fixed roles (unrolled); x one chunk ahead.
+  for (uint32_t ch = 0; ch < chunks; ch += 2) {
+    __syncthreads();  // the previous chunk's operands are consumed
+    tile.stage(xr, xs);
+    __syncthreads();
+    if (ch + 1 < chunks) tile.load_x(ch + 1, xr);
+    tile.compute(wa, xs, acc);
+    tile.load_w(ch + 2, wa);
+    if (ch + 1 >= chunks) break;
+    __syncthreads();
+    tile.stage(xr, xs);
+    __syncthreads();
+    if (ch + 2 < chunks) tile.load_x(ch + 2, xr);
+    tile.compute(wb, xs, acc);
+    tile.load_w(ch + 3, wb);
+  }
+  tile.epilogue(acc);
+}
+
+}  // namespace
+
+#define GEMM_KERNEL(NAME, WT, MODE)                                                \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemm p) { \
+    gemm<WT, MODE>(p);                                                           \
+  }
+
+GEMM_KERNEL(ammon_gemm_bf16_plain, uint16_t, AMMON_GEMV_PLAIN)
+GEMM_KERNEL(ammon_gemm_bf16_residual, uint16_t, AMMON_GEMV_RESIDUAL)
+GEMM_KERNEL(ammon_gemm_bf16_swiglu, uint16_t, AMMON_GEMV_SWIGLU)
+GEMM_KERNEL(ammon_gemm_bf16_qkv, uint16_t, AMMON_GEMV_QKV)
+GEMM_KERNEL(ammon_gemm_f32_plain, float, AMMON_GEMV_PLAIN)
+GEMM_KERNEL(ammon_gemm_f32_residual, float, AMMON_GEMV_RESIDUAL)
+GEMM_KERNEL(ammon_gemm_f32_swiglu, float, AMMON_GEMV_SWIGLU)
+GEMM_KERNEL(ammon_gemm_f32_qkv, float, AMMON_GEMV_QKV)

@@ -40,6 +40,8 @@ struct Kernels {
   hipFunction_t fill_const = nullptr;
   // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
   hipFunction_t token[2][kAttGroups] = {};
+  // prefill GEMMs on matrix cores: [weight dtype][mode]
+  hipFunction_t gemm[2][kGemvModes] = {};
 };
 
 // LDS per compute unit on gfx950 (bytes); bounds resident GEMV workgroups.

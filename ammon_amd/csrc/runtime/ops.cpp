@@ -30,15 +30,21 @@ inline bool overlaps(const void *a, size_t abytes, const void *b, size_t bbytes)
 }
 
 template <typename P>
-ammon_status launch(ammon_runtime *rt, ammon_stream s, hipFunction_t f, uint32_t gx, uint32_t gy,
-                    uint32_t shmem, P &params, const char *what) {
-  if (gx == 0 || gy == 0) return AMMON_OK;
+ammon_status launch3(ammon_runtime *rt, ammon_stream s, hipFunction_t f, uint32_t gx, uint32_t gy,
+                     uint32_t gz, uint32_t shmem, P &params, const char *what) {
+  if (gx == 0 || gy == 0 || gz == 0) return AMMON_OK;
   DeviceGuard guard(rt->device);
   hipStream_t st = s ? (hipStream_t)s : rt->stream;
   void *args[] = {&params};
-  hipError_t e = hipModuleLaunchKernel(f, gx, gy, 1, kWorkgroup, 1, 1, shmem, st, args, nullptr);
+  hipError_t e = hipModuleLaunchKernel(f, gx, gy, gz, kWorkgroup, 1, 1, shmem, st, args, nullptr);
   if (e != hipSuccess) return hip_error(e, what);
   return AMMON_OK;
+}
+
+template <typename P>
+ammon_status launch(ammon_runtime *rt, ammon_stream s, hipFunction_t f, uint32_t gx, uint32_t gy,
+                    uint32_t shmem, P &params, const char *what) {
+  return launch3(rt, s, f, gx, gy, 1, shmem, params, what);
 }
 
 #define REQUIRE_RT()                                              \
@@ -164,6 +170,19 @@ int att_group_index(uint32_t g) {
   if (g <= 4) return 2;
   if (g <= 8) return 3;
   return -1;
+}
+
+// Pass-1 variant for a cache layout, or NULL when no chunk width fits.
+hipFunction_t attention_kernel(ammon_runtime *rt, ammon_dtype kv_dtype, uint32_t q_heads,
+                               uint32_t kv_heads, uint32_t head, const void *k, const void *v) {
+  const int ci = att_chunk_index(kv_dtype, head, k, v);
+  if (ci < 0) return nullptr;
+  const int gi = att_group_index(q_heads / kv_heads);
+  const int dt = kv_dtype == AMMON_BF16 ? 1 : 0;
+  const uint32_t g = q_heads / kv_heads;
+  // head 128, widest chunk, power-of-two group: the compile-time variant
+  const bool h128 = head == 128 && ci == (dt ? 0 : 1) && (g & (g - 1)) == 0;
+  return h128 ? rt->k.att_partial_h128[dt][gi] : rt->k.att_partial[dt][ci][gi];
 }
 
 ammon_status attention_check(ammon_runtime *rt, const char *what, uint32_t q_heads,
@@ -301,18 +320,12 @@ ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, con
   AMMON_CHECK(valid_dtype(kv_dtype), "attention_partial: unknown kv dtype %d", (int)kv_dtype);
   ammon_status st = attention_check(rt, "attention_partial", q_heads, kv_heads, head, seq, split_len);
   if (st != AMMON_OK) return st;
-  const int ci = att_chunk_index(kv_dtype, head, k_cache, v_cache);
-  AMMON_CHECK(ci >= 0, "attention_partial: head %u needs an even width above 64", head);
-  const int gi = att_group_index(q_heads / kv_heads);
+  hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache);
+  AMMON_CHECK(f, "attention_partial: head %u needs an even width above 64", head);
   VALIDATE_ONLY();
   const uint32_t splits = ammon_attention_splits(seq, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, nullptr,
-                         q_heads, kv_heads, head, seq, split_len, splits};
-  const int dt = kv_dtype == AMMON_BF16 ? 1 : 0;
-  const uint32_t g = q_heads / kv_heads;
-  // head 128, widest chunk, power-of-two group: the compile-time variant
-  const bool h128 = head == 128 && ci == (dt ? 0 : 1) && (g & (g - 1)) == 0;
-  hipFunction_t f = h128 ? rt->k.att_partial_h128[dt][gi] : rt->k.att_partial[dt][ci][gi];
+                         q_heads, kv_heads, head, seq, split_len, splits, 0};
   return launch(rt, stream, f, splits, kv_heads, 0, p, "attention_partial");
 }
 
@@ -335,7 +348,7 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
-                         ammon_attention_splits(seq, split_len)};
+                         ammon_attention_splits(seq, split_len), 0};
   return launch(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), 0, p,
                 "attention_combine");
 }
@@ -363,6 +376,191 @@ ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, cons
                                seq, step, split_len, partial);
   if (st != AMMON_OK) return st;
   return ammon_attention_combine(rt, stream, partial, q_heads, head, seq, step, split_len, out);
+}
+
+// ---- prompt prefill ---------------------------------------------------------------------
+size_t ammon_attention_prefill_scratch_bytes(uint32_t tokens, uint32_t q_heads, uint32_t head,
+                                             uint32_t ctx, uint32_t split_len) {
+  return (size_t)tokens * ammon_attention_scratch_bytes(q_heads, head, ctx, split_len);
+}
+
+ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, const float *q,
+                                     uint32_t tokens, uint32_t q_heads, const void *k_cache,
+                                     const void *v_cache, ammon_dtype kv_dtype, uint32_t kv_heads,
+                                     uint32_t head, uint32_t seq, const ammon_decode_step *step,
+                                     uint32_t ctx, uint32_t split_len, float *partial,
+                                     size_t partial_bytes, float *out) {
+  REQUIRE_RT();
+  AMMON_CHECK(q && k_cache && v_cache && step && partial && out,
+              "attention_prefill: NULL q, cache, step, partial or out");
+  AMMON_CHECK(valid_dtype(kv_dtype), "attention_prefill: unknown kv dtype %d", (int)kv_dtype);
+  AMMON_CHECK(tokens > 0, "attention_prefill: no query tokens");
+  ammon_status st = attention_check(rt, "attention_prefill", q_heads, kv_heads, head, seq, split_len);
+  if (st != AMMON_OK) return st;
+  AMMON_CHECK(ctx >= 1 && ctx <= seq, "attention_prefill: ctx %u outside [1, seq=%u]", ctx, seq);
+  const size_t need = ammon_attention_prefill_scratch_bytes(tokens, q_heads, head, ctx, split_len);
+  AMMON_CHECK(partial_bytes >= need, "attention_prefill: partial scratch must be %zu bytes", need);
+  const size_t qbytes = (size_t)tokens * q_heads * head * 4;
+  AMMON_CHECK(!overlaps(out, qbytes, q, qbytes) && !overlaps(out, qbytes, partial, need) &&
+                  !overlaps(q, qbytes, partial, need),
+              "attention_prefill: q, partial and out must not overlap");
+  hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache);
+  AMMON_CHECK(f, "attention_prefill: head %u needs an even width above 64", head);
+  VALIDATE_ONLY();
+  // the partial layout and the grid cover ctx positions: [tokens][q_heads][splits][head + 2]
+  const uint32_t splits = ammon_attention_splits(ctx, split_len);
+  ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, out,
+                         q_heads, kv_heads, head, seq, split_len, splits, 0};
+  st = launch3(rt, stream, f, splits, kv_heads, tokens, 0, p, "attention_prefill");
+  if (st != AMMON_OK) return st;
+  return launch3(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), tokens, 0, p,
+                 "attention_prefill");
+}
+
+namespace {
+
+struct GemmArgs {
+  int mode;
+  const void *w0, *w1, *w2;
+  ammon_dtype w_dtype;
+  uint32_t d, n, rows, tokens;
+  const float *x;
+  const float *residual;
+  float *y;
+  size_t y_bytes;
+  void *k_cache, *v_cache;
+  const ammon_decode_step *step;
+  const float *table;
+  uint32_t kv_dim, head, seq;
+  ammon_dtype kv_dtype;
+};
+
+ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemmArgs &a,
+                                   const char *what) {
+  AMMON_CHECK(valid_dtype(a.w_dtype), "%s: unknown weight dtype %d", what, (int)a.w_dtype);
+  AMMON_CHECK(a.w0 && a.x && a.y, "%s: NULL weight, x or y", what);
+  AMMON_CHECK(a.n > 0 && a.d > 0 && a.tokens > 0, "%s: empty shape (d=%u, n=%u, tokens=%u)", what,
+              a.d, a.n, a.tokens);
+  AMMON_CHECK(a.n % 8 == 0, "%s: reduction length %u must be a multiple of 8", what, a.n);
+  AMMON_CHECK((uint64_t)a.n * 32 * 4 < (1ull << 31), "%s: reduction length %u too large", what,
+              a.n);
+  AMMON_CHECK(a.rows < (1u << 31), "%s: too many rows", what);
+  const uintptr_t bits = (uintptr_t)a.w0 | (uintptr_t)a.w1 | (uintptr_t)a.w2 | (uintptr_t)a.x;
+  AMMON_CHECK((bits & 15u) == 0, "%s: weights and x must be 16-byte aligned", what);
+  const size_t xbytes = (size_t)a.tokens * a.n * 4;
+  AMMON_CHECK(!overlaps(a.x, xbytes, a.y, a.y_bytes), "%s: y overlaps x", what);
+  if (a.residual)
+    AMMON_CHECK(!overlaps(a.x, xbytes, a.residual, a.y_bytes), "%s: residual overlaps x", what);
+  VALIDATE_ONLY();
+  ammon_k_gemm p = {};
+  p.w0 = a.w0;
+  p.w1 = a.w1;
+  p.w2 = a.w2;
+  p.x = a.x;
+  p.residual = a.residual;
+  p.y = a.y;
+  p.k_cache = a.k_cache;
+  p.v_cache = a.v_cache;
+  p.step = (const ammon_k_step *)a.step;
+  p.table = a.table;
+  p.d = a.d;
+  p.n = a.n;
+  p.rows = a.rows;
+  p.tokens = a.tokens;
+  p.kv_dim = a.kv_dim;
+  p.head = a.head;
+  p.seq = a.seq;
+  p.kv_dtype = (uint32_t)a.kv_dtype;
+  hipFunction_t f = rt->k.gemm[a.w_dtype == AMMON_BF16 ? 1 : 0][a.mode];
+  // 64 virtual rows x 32 tokens per workgroup
+  return launch(rt, stream, f, cdiv(a.rows, 64), cdiv(a.tokens, 32), 0, p, what);
+}
+
+}  // namespace
+
+ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                uint32_t tokens, float *y, const float *residual) {
+  REQUIRE_RT();
+  GemmArgs a = {};
+  a.mode = residual ? AMMON_GEMV_RESIDUAL : AMMON_GEMV_PLAIN;
+  a.w0 = w;
+  a.w_dtype = w_dtype;
+  a.d = d;
+  a.n = n;
+  a.rows = d;
+  a.tokens = tokens;
+  a.x = x;
+  a.residual = residual;
+  a.y = y;
+  a.y_bytes = (size_t)tokens * d * 4;
+  return gemm_check_and_launch(rt, stream, a, "prefill_gemm");
+}
+
+ammon_status ammon_prefill_qkv_rope_store(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *wq, const void *wk,
+                                          const void *wv, ammon_dtype w_dtype, uint32_t dim,
+                                          uint32_t q_heads, uint32_t kv_heads, uint32_t head,
+                                          float *q, void *k_cache, void *v_cache,
+                                          ammon_dtype kv_dtype, uint32_t seq,
+                                          const ammon_decode_step *step, const float *table) {
+  REQUIRE_RT();
+  AMMON_CHECK(wq && wk && wv, "prefill_qkv: NULL wq, wk or wv");
+  AMMON_CHECK(k_cache && v_cache && step && table, "prefill_qkv: NULL cache, step or table");
+  AMMON_CHECK(valid_dtype(kv_dtype), "prefill_qkv: unknown kv dtype %d", (int)kv_dtype);
+  AMMON_CHECK(head >= 16 && head % 16 == 0, "prefill_qkv: head size %u must be a multiple of 16",
+              head);
+  AMMON_CHECK(q_heads > 0 && kv_heads > 0 && seq > 0, "prefill_qkv: empty shape");
+  const uint64_t q_dim = (uint64_t)q_heads * head, kv_dim = (uint64_t)kv_heads * head;
+  AMMON_CHECK(kv_dim <= q_dim, "attention: kv width must be even and no wider than q");
+  AMMON_CHECK(q_dim + 2 * kv_dim < (1ull << 31), "prefill_qkv: too many rows");
+  AMMON_CHECK(!overlaps(k_cache, (size_t)kv_dim * seq * dsize(kv_dtype), v_cache,
+                        (size_t)kv_dim * seq * dsize(kv_dtype)),
+              "prefill_qkv: key and value caches overlap");
+  GemmArgs a = {};
+  a.mode = AMMON_GEMV_QKV;
+  a.w0 = wq;
+  a.w1 = wk;
+  a.w2 = wv;
+  a.w_dtype = w_dtype;
+  a.d = (uint32_t)q_dim;
+  a.n = dim;
+  a.rows = (uint32_t)(q_dim + 2 * kv_dim);
+  a.tokens = tokens;
+  a.x = x;
+  a.y = q;
+  a.y_bytes = (size_t)tokens * q_dim * 4;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.step = step;
+  a.table = table;
+  a.kv_dim = (uint32_t)kv_dim;
+  a.head = head;
+  a.seq = seq;
+  a.kv_dtype = kv_dtype;
+  return gemm_check_and_launch(rt, stream, a, "prefill_qkv_rope_store");
+}
+
+ammon_status ammon_prefill_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *w1, const void *w3,
+                                          ammon_dtype w_dtype, uint32_t dim, uint32_t hidden,
+                                          float *hb) {
+  REQUIRE_RT();
+  AMMON_CHECK(w1 && w3, "prefill_gate_up_swiglu: NULL w1 or w3");
+  AMMON_CHECK((uint64_t)hidden * 2 < (1ull << 31), "prefill_gate_up_swiglu: too many rows");
+  GemmArgs a = {};
+  a.mode = AMMON_GEMV_SWIGLU;
+  a.w0 = w1;
+  a.w1 = w3;
+  a.w_dtype = w_dtype;
+  a.d = hidden;
+  a.n = dim;
+  a.rows = 2 * hidden;
+  a.tokens = tokens;
+  a.x = x;
+  a.y = hb;
+  a.y_bytes = (size_t)tokens * hidden * 4;
+  return gemm_check_and_launch(rt, stream, a, "prefill_gate_up_swiglu");
 }
 
 // ---- elementwise ---------------------------------------------------------------------------

@@ -27,6 +27,7 @@ AMMON_BLOB(attention)
 AMMON_BLOB(gemv)
 AMMON_BLOB(misc)
 AMMON_BLOB(token)
+AMMON_BLOB(prefill)
 
 namespace ammon_rt {
 
@@ -79,7 +80,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   } blobs[] = {{"embed", ammon_co_embed}, {"norm", ammon_co_norm},
                {"rope", ammon_co_rope},   {"attention", ammon_co_attention},
                {"gemv", ammon_co_gemv},   {"misc", ammon_co_misc},
-               {"token", ammon_co_token}};
+               {"token", ammon_co_token}, {"prefill", ammon_co_prefill}};
   constexpr int kModules = (int)(sizeof(blobs) / sizeof(blobs[0]));
   hipModule_t mods[kModules];
   for (int i = 0; i < kModules; ++i) {
@@ -135,6 +136,12 @@ static ammon_status load_kernels(ammon_runtime *rt) {
       char name[96];
       snprintf(name, sizeof name, "ammon_token_bf16_kv%s_g%d", dtn[d], gs[g]);
       R(6, name, k.token[d][g]);
+    }
+  for (int d = 0; d < 2; ++d)
+    for (int m = 0; m < kGemvModes; ++m) {
+      char name[96];
+      snprintf(name, sizeof name, "ammon_gemm_%s_%s", dtn[d], modes[m]);
+      R(7, name, k.gemm[d][m]);
     }
 #undef R
   return AMMON_OK;

@@ -118,6 +118,21 @@ class LlamaModel:
         return self._generate("ammon_llama_generate_tokens_device", prompt, max_new_tokens,
                               stop_on)
 
+    def generate_tokens_prefill(self, prompt, max_new_tokens: int, stop_on=None):
+        """Same loop with the prompt prefilled in one pass (GEMMs on matrix
+        cores, token-batched attention) before the device greedy steps."""
+        return self._generate("ammon_llama_generate_tokens_prefill", prompt, max_new_tokens,
+                              stop_on)
+
+    def prefill(self, tokens, start_pos: int = 0) -> np.ndarray:
+        """Run tokens at positions start_pos.. in one pass; the last
+        position's logits."""
+        tokens = np.ascontiguousarray(tokens, dtype=np.int32)
+        logits = np.empty(self.cfg.vocab, np.float32)
+        call("ammon_llama_prefill", self.handle, tokens.ctypes.data, tokens.size, start_pos,
+             logits.ctypes.data)
+        return logits
+
     def decode(self, token: int, start_pos: int, n_steps: int, read_tokens: bool = False):
         """Enqueue n_steps device-greedy steps from (token, start_pos)."""
         toks = np.empty(n_steps, np.int32) if read_tokens else None

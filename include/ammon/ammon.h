@@ -287,6 +287,49 @@ ammon_status ammon_greedy_next(ammon_runtime *rt, ammon_stream stream, const flo
                                uint32_t n_prompt, ammon_decode_step *step, int32_t *tokens,
                                uint32_t max_tokens);
 
+/* ---- prompt prefill -------------------------------------------------------
+ * No counterpart kernels in the reference, which feeds a prompt one decode
+ * step per token (src/generate.rs:62-64).  These run `tokens` consecutive
+ * positions step->position + t (t < tokens) at once with the decode path's
+ * per-token arithmetic: the same formulas and fp32-grade products, the
+ * projections as GEMMs on matrix cores (so only the fp32 summation order
+ * differs from the GEMVs).  x, q, hb, y: row-major [tokens, width] fp32,
+ * 16-byte aligned; the reduction length n (dim or hidden) a multiple of 8. */
+
+/* The GEMV of ammon_gemv over rows of x: y[t] = W x[t] (+ residual[t]);
+ * residual may equal y. */
+ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                uint32_t tokens, float *y, const float *residual);
+/* ammon_qkv_rope_store over rows of an already normalised x: q [tokens,
+ * q_heads * head]; rotated k and raw v rows go to the caches at positions
+ * step->position + t.  head a multiple of 16. */
+ammon_status ammon_prefill_qkv_rope_store(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *wq, const void *wk,
+                                          const void *wv, ammon_dtype w_dtype, uint32_t dim,
+                                          uint32_t q_heads, uint32_t kv_heads, uint32_t head,
+                                          float *q, void *k_cache, void *v_cache,
+                                          ammon_dtype kv_dtype, uint32_t seq,
+                                          const ammon_decode_step *step, const float *table);
+/* ammon_gate_up_swiglu over rows of an already normalised x: hb [tokens,
+ * hidden]. */
+ammon_status ammon_prefill_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *w1, const void *w3,
+                                          ammon_dtype w_dtype, uint32_t dim, uint32_t hidden,
+                                          float *hb);
+/* ammon_attention_decode for each of `tokens` query rows q [tokens, q_heads,
+ * head] at positions step->position + t, which must be below ctx <= seq
+ * (the scratch and the grid cover ctx positions); out [tokens, q_heads,
+ * head].  `partial` holds ammon_attention_prefill_scratch_bytes bytes. */
+size_t ammon_attention_prefill_scratch_bytes(uint32_t tokens, uint32_t q_heads, uint32_t head,
+                                             uint32_t ctx, uint32_t split_len);
+ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, const float *q,
+                                     uint32_t tokens, uint32_t q_heads, const void *k_cache,
+                                     const void *v_cache, ammon_dtype kv_dtype, uint32_t kv_heads,
+                                     uint32_t head, uint32_t seq, const ammon_decode_step *step,
+                                     uint32_t ctx, uint32_t split_len, float *partial,
+                                     size_t partial_bytes, float *out);
+
 #ifdef __cplusplus
 }
 #endif

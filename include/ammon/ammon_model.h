@@ -80,6 +80,26 @@ ammon_status ammon_llama_generate_tokens_device(ammon_llama *m, const int32_t *p
                                                 int32_t *out_tokens, uint32_t *n_out,
                                                 double *tokens_per_second, float *last_logits);
 
+/* Prompt prefill (no counterpart in the reference, which steps the prompt
+ * one token at a time, src/generate.rs:62-64): tokens[0..n) run at
+ * positions start_pos.. in one pass per layer (GEMMs on matrix cores,
+ * token-batched attention), filling the KV cache; the DecodeStep is left at
+ * {tokens[n - 1], start_pos + n - 1} as after stepping them one by one.
+ * logits (nullable, host, [vocab]) receives the last position's logits. */
+ammon_status ammon_llama_prefill(ammon_llama *m, const int32_t *tokens, uint32_t n,
+                                 uint32_t start_pos, float *logits);
+
+/* generate_tokens_device with the prompt prefilled in one pass: the same
+ * outputs (up to fp32 summation order in the prompt's projections), with
+ * the prompt's positions in one launch per kernel instead of one decode
+ * step each.  tokens_per_second covers the decode steps after the first
+ * generated token. */
+ammon_status ammon_llama_generate_tokens_prefill(ammon_llama *m, const int32_t *prompt,
+                                                 uint32_t n_prompt, uint32_t max_new_tokens,
+                                                 int has_stop, int32_t stop_on,
+                                                 int32_t *out_tokens, uint32_t *n_out,
+                                                 double *tokens_per_second, float *last_logits);
+
 /* Enqueue `n_steps` device-greedy decode steps starting from (token,
  * start_pos) on the model's stream, without synchronising (the caller times
  * them with events).  tokens (nullable, host, [n_steps]) is filled after an
