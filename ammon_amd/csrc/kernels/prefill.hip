@@ -5,12 +5,16 @@
 // 518-528, serial definition :54-73) per token.  Prefill runs T consecutive
 // positions through one GEMM per projection, Y[t] = W X[t], with the decode
 // GEMV's fused epilogues: PLAIN, RESIDUAL (y = residual + W x), SWIGLU (gate
-// and up rows, silu(gate) * up as src/kernels.rs:472-475) and QKV (RoPE on
+// rows in waves 0-1, the matching up rows in waves 2-3, paired through LDS:
+// silu(gate) * up as src/kernels.rs:472-475) and QKV (RoPE on
 // (2i, 2i+1) pairs of q and k rows at position step->position + t, then the
 // head-major K/V cache stores of src/kernels.rs:174-226).
 //
-// Tiling.  A workgroup owns 64 virtual rows (16 per wave) x 32 tokens (two
-// 16-token column tiles) and walks the reduction in 256-wide chunks.  On
+// Tiling.  A workgroup owns 64 virtual rows (16 per wave) x 16 NT tokens
+// (NT 16-token column tiles) and walks the reduction in KC-wide chunks: NT = 1,
+// KC = 512 for prompts of up to 16 tokens (twice the W bytes in flight per
+// wave: x staging waits on the loads issued before it, so the W chunk after
+// the current one is all a wave keeps in flight), NT = 2, KC = 256 beyond.  On
 // each 32-wide step a wave multiplies its 16 x 32 slice of W (the A operand,
 // as stored: lane l holds row l % 16, k 8(l / 16)..+7) by the tokens' x (the
 // B operand, lane l: token l % 16, the same k) with 16x16 MFMAs; lane l then
@@ -29,11 +33,15 @@
 // chunks in flight per wave.  x is read from L2 (it is small and every
 // workgroup of the pass reads it), one chunk ahead in registers, split /
 // packed, and staged in LDS in the B-operand order: quad (step s, column
-// tile c, part q, lane l) at ((s * 2 + c) * XQ + q) * 64 + l, so every
+// tile c, part q, lane l) at ((s * NT + c) * XQ + q) * 64 + l, so every
 // operand read is a conflict-free ds_read_b128.  Column tiles past the last
 // token are skipped.
 //
-// Launch: grid (ceil(rows / 64), ceil(tokens / 32)), 256 threads.
+// Launch: a 1-D grid of ceil(row blocks / 8) * 8 * token tiles workgroups of
+// 256 threads.  Workgroups go to the 8 XCDs round robin (id % 8), each XCD
+// with its own L2, so the id -> (row block, token tile) map keeps all token
+// tiles of a row block on one XCD and adjacent in dispatch order: W is
+// fetched from HBM about once and re-read from that XCD's L2.
 #include "device_common.h"
 
 namespace {
@@ -41,11 +49,6 @@ namespace {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x8 __attribute__((ext_vector_type(8)));
 
-constexpr uint32_t KC = 256;        // reduction chunk
-constexpr uint32_t S = KC / 32;     // 32-wide steps per chunk
-constexpr uint32_t NT = 2;          // 16-token column tiles per workgroup
-constexpr uint32_t TB = 16 * NT;    // tokens per workgroup
-constexpr uint32_t RB = 16 * AMMON_WAVES;  // virtual rows per workgroup
 
 // WQ: 16-byte W loads per lane per step; XQ: LDS quads per lane per (step,
 // column tile) -- three bf16 parts of 8 x values, or 8 fp32 x values.
@@ -57,38 +60,49 @@ template <> struct GemmTraits<float> {
   static constexpr int WQ = 2, XQ = 2;
 };
 
-template <typename WT, int MODE>
+// NT 16-token column tiles per workgroup, KC-wide reduction chunks; KS
+// waves share a row tile, each taking every KS-th 32-wide step (KS = 4: one
+// 16-row tile per workgroup, the four partial sums added in wave order).
+template <typename WT, int MODE, uint32_t NT, uint32_t KC, uint32_t KS>
 struct GemmTile {
   static constexpr int WQ = GemmTraits<WT>::WQ, XQ = GemmTraits<WT>::XQ;
   static constexpr uint32_t ES = sizeof(WT);
+  static constexpr uint32_t S = KC / 32;     // 32-wide steps per chunk
+  static constexpr uint32_t SW = S / KS;     // of which each wave takes
+  static constexpr uint32_t RBW = 16 * AMMON_WAVES / KS;  // virtual rows per workgroup
+  static constexpr uint32_t TB = 16 * NT;    // tokens per workgroup
+  static constexpr uint32_t KG = KC / 8;     // 8-wide k groups per chunk
+  static constexpr uint32_t XU = TB * KG / AMMON_WG;  // x units per thread per chunk
+  static_assert(TB * KG % AMMON_WG == 0, "x units per thread");
 
   ammon_k_gemm p;  // by value: a reference to the kernel argument would live in scratch
-  uint32_t lane, wave, vr0, tok0, row_bytes;
-  // W source of this wave: lane row `lr` of resource r0 (or r1 for the up
-  // rows of SWIGLU)
+  uint32_t lane, wave, kw, vr0, tok0, row_bytes;
+  // W source of this wave: row lane % 16 of resource r0.  SWIGLU, KS = 1:
+  // waves 0-1 take gate rows i0..i0+15 / +16..+31 of the workgroup's 32
+  // hidden rows, waves 2-3 the same up rows; KS = 4: rows 0-7 of the tile
+  // are gate rows i0..i0+7 (r0), rows 8-15 the same up rows (r1).  vr0 is
+  // then the first hidden row.
   __amdgpu_buffer_rsrc_t r0, r1;
-  uint32_t lr;
-  bool use_r1;
 
-  AMMON_DEV GemmTile(const ammon_k_gemm &p_) : p(p_) {
+  AMMON_DEV GemmTile(const ammon_k_gemm &p_, uint32_t rb, uint32_t tt) : p(p_) {
     lane = threadIdx.x & 63;
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    vr0 = blockIdx.x * RB + 16 * wave;
-    tok0 = blockIdx.y * TB;
+    kw = wave % KS;
+    vr0 = rb * RBW + 16 * (wave / KS);
+    tok0 = tt * TB;
     row_bytes = p.n * ES;
-    lr = lane & 15;
-    use_r1 = false;
     auto rsrc = [&](const void *base, uint32_t first, uint32_t limit, uint32_t count) {
       const uint32_t valid = first < limit ? min(count, limit - first) : 0;
       return make_rsrc((const WT *)base + (size_t)(valid ? first : 0) * p.n, valid * row_bytes);
     };
-    if (MODE == AMMON_GEMV_SWIGLU) {
-      // rows 0-7 of the wave tile: gate rows i0.., rows 8-15: up rows i0..
-      const uint32_t i0 = vr0 / 2;
-      r0 = rsrc(p.w0, i0, p.d, 8);
-      r1 = rsrc(p.w1, i0, p.d, 8);
-      use_r1 = lr >= 8;
-      lr &= 7;
+    r1 = r0 = make_rsrc(p.w0, 0);
+    if (MODE == AMMON_GEMV_SWIGLU && KS == 1) {
+      vr0 = rb * (RBW / 2) + 16 * (wave & 1);
+      r0 = rsrc(wave >= 2 ? p.w1 : p.w0, vr0, p.d, 16);
+    } else if (MODE == AMMON_GEMV_SWIGLU) {
+      vr0 = rb * (RBW / 2);
+      r0 = rsrc(p.w0, vr0, p.d, 8);
+      r1 = rsrc(p.w1, vr0, p.d, 8);
     } else if (MODE == AMMON_GEMV_QKV) {
       const uint32_t kvd = p.kv_dim;
       if (vr0 < p.d)
@@ -97,42 +111,43 @@ struct GemmTile {
         r0 = rsrc(p.w1, vr0 - p.d, kvd, 16);
       else
         r0 = rsrc(p.w2, vr0 - p.d - kvd, kvd, 16);
-      r1 = r0;
     } else {
       r0 = rsrc(p.w0, vr0, p.rows, 16);
-      r1 = r0;
     }
   }
 
-  // W quads of chunk `ch` (k past the row end read as zero).
-  AMMON_DEV void load_w(uint32_t ch, u32x4 (&w)[S][WQ]) const {
+  // W quads of this wave's steps of chunk `ch` (k past the row end read as
+  // zero).
+  AMMON_DEV void load_w(uint32_t ch, u32x4 (&w)[SW][WQ]) const {
 #pragma unroll
-    for (uint32_t s = 0; s < S; ++s) {
-      const uint32_t k = ch * KC + 32 * s + 8 * (lane >> 4);
+    for (uint32_t j = 0; j < SW; ++j) {
+      const uint32_t k = ch * KC + 32 * (j * KS + kw) + 8 * (lane >> 4);
       const bool ok = k < p.n;
 #pragma unroll
       for (int q = 0; q < WQ; ++q) {
-        const uint32_t off = lr * row_bytes + (k + 4 * q) * ES;
-        if (MODE == AMMON_GEMV_SWIGLU) {
-          // both resources, each lane's other one out of range: no branch
-          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r0, ok && !use_r1 ? off : AMMON_OOB, 0, 0);
-          const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r1, ok && use_r1 ? off : AMMON_OOB, 0, 0);
-          w[s][q] = a | b;
+        if (MODE == AMMON_GEMV_SWIGLU && KS > 1) {
+          // gate lanes read r0, up lanes r1; each lane's other one out of range
+          const uint32_t off = (lane & 7) * row_bytes + (k + 4 * q) * ES;
+          const bool up = (lane & 15) >= 8;
+          const u32x4 a = __builtin_amdgcn_raw_buffer_load_b128(r0, ok && !up ? off : AMMON_OOB, 0, 0);
+          const u32x4 b = __builtin_amdgcn_raw_buffer_load_b128(r1, ok && up ? off : AMMON_OOB, 0, 0);
+          w[j][q] = a | b;
         } else {
-          w[s][q] = __builtin_amdgcn_raw_buffer_load_b128(r0, ok ? off : AMMON_OOB, 0, 0);
+          const uint32_t off = (lane & 15) * row_bytes + (k + 4 * q) * ES;
+          w[j][q] = __builtin_amdgcn_raw_buffer_load_b128(r0, ok ? off : AMMON_OOB, 0, 0);
         }
       }
     }
   }
 
-  // x of chunk `ch`: unit u = tid + 256 m is (token u / 32, 8-wide k group
-  // u % 32); tokens and k past the end read as zero (no branches).
-  AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[4][2]) const {
+  // x of chunk `ch`: unit u = tid + 256 m is (token u / KG, 8-wide k group
+  // u % KG); tokens and k past the end read as zero (no branches).
+  AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[XU][2]) const {
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x + (size_t)tok0 * p.n, (min(p.tokens - tok0, TB)) * p.n * 4);
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (uint32_t m = 0; m < XU; ++m) {
       const uint32_t u = threadIdx.x + AMMON_WG * m;
-      const uint32_t t = u >> 5, k = ch * KC + 8 * (u & 31);
+      const uint32_t t = u / KG, k = ch * KC + 8 * (u % KG);
       const uint32_t off = k < p.n ? (t * p.n + k) * 4 : AMMON_OOB;
       x[m][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
       x[m][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
@@ -144,11 +159,11 @@ struct GemmTile {
   }
 
   // Split / pack the x chunk into LDS in B-operand order.
-  AMMON_DEV void stage(const u32x4 (&x)[4][2], u32x4 *xs) const {
+  AMMON_DEV void stage(const u32x4 (&x)[XU][2], u32x4 *xs) const {
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
+    for (uint32_t m = 0; m < XU; ++m) {
       const uint32_t u = threadIdx.x + AMMON_WG * m;
-      const uint32_t t = u >> 5, kg = u & 31;
+      const uint32_t t = u / KG, kg = u % KG;
       const uint32_t s = kg >> 2, c = t >> 4, l = (t & 15) + 16 * (kg & 3);
       if constexpr (sizeof(WT) == 2) {
         const f32x4 a = __builtin_bit_cast(f32x4, x[m][0]), b = __builtin_bit_cast(f32x4, x[m][1]);
@@ -168,14 +183,15 @@ struct GemmTile {
     }
   }
 
-  AMMON_DEV void compute(const u32x4 (&w)[S][WQ], const u32x4 *xs, f32x4 (&acc)[NT]) const {
+  AMMON_DEV void compute(const u32x4 (&w)[SW][WQ], const u32x4 *xs, f32x4 (&acc)[NT]) const {
 #pragma unroll
-    for (uint32_t s = 0; s < S; ++s) {
+    for (uint32_t j = 0; j < SW; ++j) {
+      const uint32_t s = j * KS + kw;
 #pragma unroll
       for (uint32_t c = 0; c < NT; ++c) {
         if (tok0 + 16 * c >= p.tokens) continue;  // uniform
         if constexpr (sizeof(WT) == 2) {
-          const bf16x8 a = __builtin_bit_cast(bf16x8, w[s][0]);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, w[j][0]);
 #pragma unroll
           for (int q = 0; q < 3; ++q) {
             const bf16x8 b = __builtin_bit_cast(bf16x8, xs[quad(s, c, q, lane)]);
@@ -184,7 +200,7 @@ struct GemmTile {
         } else {
 #pragma unroll
           for (int q = 0; q < 2; ++q) {
-            const f32x4 a = __builtin_bit_cast(f32x4, w[s][q]);
+            const f32x4 a = __builtin_bit_cast(f32x4, w[j][q]);
             const f32x4 b = __builtin_bit_cast(f32x4, xs[quad(s, c, q, lane)]);
 #pragma unroll
             for (int e = 0; e < 4; ++e)
@@ -196,24 +212,56 @@ struct GemmTile {
   }
 
   // Lane l holds rows 4(l / 16) + r of the wave tile, token tok0 + 16c + l % 16.
-  AMMON_DEV void epilogue(f32x4 (&acc)[NT]) const {
+  // KS = 1: contains barriers (SWIGLU), call uniformly; KS > 1: wave 0 only,
+  // with the summed partials.  xs is free by then.
+  AMMON_DEV void epilogue(f32x4 (&acc)[NT], u32x4 *xs) const {
     const uint32_t rq = 4 * (lane >> 4);
+    float *ex = (float *)xs;
+    if (MODE == AMMON_GEMV_SWIGLU && KS > 1) {
+      // gate rows sit in lanes 0-31, the matching up rows 32 lanes higher
 #pragma unroll
-    for (uint32_t c = 0; c < NT; ++c) {
-      const uint32_t t = tok0 + 16 * c + (lane & 15);
-      if (MODE == AMMON_GEMV_SWIGLU) {
-        // gate rows sit in lanes 0-31, the matching up rows 32 lanes higher
+      for (uint32_t c = 0; c < NT; ++c) {
         float up[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) up[r] = __shfl_xor(acc[c][r], 32);
+        const uint32_t t = tok0 + 16 * c + (lane & 15);
         if (lane >= 32 || t >= p.tokens) continue;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t i = vr0 / 2 + rq + r;
+          const uint32_t i = vr0 + rq + r;
           if (i >= p.d) continue;
           const float gate = acc[c][r];
           float v = gate * (1.0f / (1.0f + expf(-gate)));
           v = v * up[r];
+          p.y[(size_t)t * p.d + i] = v;
+        }
+      }
+      return;
+    }
+    if (MODE == AMMON_GEMV_SWIGLU) {
+      // waves 2-3 hand their up rows to waves 0-1 through LDS, same lane layout
+      __syncthreads();
+      if (wave >= 2) {
+#pragma unroll
+        for (uint32_t c = 0; c < NT; ++c)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ex[((((wave - 2) * NT + c) * 4) + r) * 64 + lane] = acc[c][r];
+      }
+      __syncthreads();
+      if (wave >= 2) return;
+    }
+#pragma unroll
+    for (uint32_t c = 0; c < NT; ++c) {
+      const uint32_t t = tok0 + 16 * c + (lane & 15);
+      if (MODE == AMMON_GEMV_SWIGLU) {
+        if (t >= p.tokens) continue;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t i = vr0 + rq + r;
+          if (i >= p.d) continue;
+          const float gate = acc[c][r], up = ex[(((wave * NT + c) * 4) + r) * 64 + lane];
+          float v = gate * (1.0f / (1.0f + expf(-gate)));
+          v = v * up;
           p.y[(size_t)t * p.d + i] = v;
         }
       } else if (MODE == AMMON_GEMV_QKV) {
@@ -267,17 +315,25 @@ struct GemmTile {
   }
 };
 
-template <typename WT, int MODE>
+template <typename WT, int MODE, uint32_t NT, uint32_t KC, uint32_t KS>
 AMMON_DEV void gemm(const ammon_k_gemm &p) {
-  using T = GemmTile<WT, MODE>;
+  using T = GemmTile<WT, MODE, NT, KC, KS>;
+  constexpr uint32_t S = T::S, SW = T::SW;
   __shared__ u32x4 xs[S * NT * T::XQ * 64];
-  T tile(p);
+  static_assert(S * NT * T::XQ * 64 * 4 >= (KS - 1) * NT * 4 * 64, "room for the partial sums");
+  // XCD-aware tile map: id = (row block group, token tile, XCD), row block =
+  // group * 8 + XCD
+  const uint32_t tiles = (p.tokens + T::TB - 1) / T::TB;
+  const uint32_t q = blockIdx.x >> 3;
+  const uint32_t rb = (q / tiles) * 8 + (blockIdx.x & 7u), tt = q % tiles;
+  if (rb * T::RBW >= p.rows) return;  // padding of the last group (uniform)
+  T tile(p, rb, tt);
   f32x4 acc[NT];
 #pragma unroll
   for (uint32_t c = 0; c < NT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
   const uint32_t chunks = (p.n + KC - 1) / KC;
-  u32x4 wa[S][T::WQ], wb[S][T::WQ];
-  u32x4 xr[4][2];
+  u32x4 wa[SW][T::WQ], wb[SW][T::WQ];
+  u32x4 xr[T::XU][2];
   tile.load_w(0, wa);
   tile.load_w(1, wb);
   tile.load_x(0, xr);
@@ -297,21 +353,47 @@ AMMON_DEV void gemm(const ammon_k_gemm &p) {
     tile.compute(wb, xs, acc);
     tile.load_w(ch + 3, wb);
   }
-  tile.epilogue(acc);
+  if (KS > 1) {
+    // waves 1..KS-1 hand their partial sums to wave 0, added in wave order
+    float *ex = (float *)xs;
+    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (wave > 0) {
+#pragma unroll
+      for (uint32_t c = 0; c < NT; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ex[(((wave - 1) * NT + c) * 4 + r) * 64 + lane] = acc[c][r];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (uint32_t w = 1; w < KS; ++w)
+#pragma unroll
+      for (uint32_t c = 0; c < NT; ++c)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) acc[c][r] += ex[(((w - 1) * NT + c) * 4 + r) * 64 + lane];
+  }
+  tile.epilogue(acc, xs);
 }
 
 }  // namespace
 
-#define GEMM_KERNEL(NAME, WT, MODE)                                                \
+#define GEMM_KERNEL(NAME, WT, MODE, NT, KC, KS)                                    \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemm p) { \
-    gemm<WT, MODE>(p);                                                           \
+    gemm<WT, MODE, NT, KC, KS>(p);                                               \
   }
+#define GEMM_MODE4(DT, WT, SUFFIX, NT, KC, KS)                                         \
+  GEMM_KERNEL(ammon_gemm_##DT##_plain_##SUFFIX, WT, AMMON_GEMV_PLAIN, NT, KC, KS)       \
+  GEMM_KERNEL(ammon_gemm_##DT##_residual_##SUFFIX, WT, AMMON_GEMV_RESIDUAL, NT, KC, KS) \
+  GEMM_KERNEL(ammon_gemm_##DT##_swiglu_##SUFFIX, WT, AMMON_GEMV_SWIGLU, NT, KC, KS)     \
+  GEMM_KERNEL(ammon_gemm_##DT##_qkv_##SUFFIX, WT, AMMON_GEMV_QKV, NT, KC, KS)
+// t16 / t32: up to 16 / 32 tokens per workgroup; k4: one 16-row tile per
+// workgroup, the reduction split over its four waves
+#define GEMM_MODES(DT, WT, KC16)              \
+  GEMM_MODE4(DT, WT, t16, 1, KC16, 1)         \
+  GEMM_MODE4(DT, WT, t32, 2, 256, 1)          \
+  GEMM_MODE4(DT, WT, t16_k4, 1, KC16, 4)      \
+  GEMM_MODE4(DT, WT, t32_k4, 2, 256, 4)
 
-GEMM_KERNEL(ammon_gemm_bf16_plain, uint16_t, AMMON_GEMV_PLAIN)
-GEMM_KERNEL(ammon_gemm_bf16_residual, uint16_t, AMMON_GEMV_RESIDUAL)
-GEMM_KERNEL(ammon_gemm_bf16_swiglu, uint16_t, AMMON_GEMV_SWIGLU)
-GEMM_KERNEL(ammon_gemm_bf16_qkv, uint16_t, AMMON_GEMV_QKV)
-GEMM_KERNEL(ammon_gemm_f32_plain, float, AMMON_GEMV_PLAIN)
-GEMM_KERNEL(ammon_gemm_f32_residual, float, AMMON_GEMV_RESIDUAL)
-GEMM_KERNEL(ammon_gemm_f32_swiglu, float, AMMON_GEMV_SWIGLU)
-GEMM_KERNEL(ammon_gemm_f32_qkv, float, AMMON_GEMV_QKV)
+GEMM_MODES(bf16, uint16_t, 512)
+GEMM_MODES(f32, float, 256)

@@ -40,8 +40,9 @@ struct Kernels {
   hipFunction_t fill_const = nullptr;
   // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
   hipFunction_t token[2][kAttGroups] = {};
-  // prefill GEMMs on matrix cores: [weight dtype][mode]
-  hipFunction_t gemm[2][kGemvModes] = {};
+  // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]
+  // [row tile per wave / split over the workgroup's waves][mode]
+  hipFunction_t gemm[2][2][2][kGemvModes] = {};
 };
 
 // LDS per compute unit on gfx950 (bytes); bounds resident GEMV workgroups.
@@ -88,6 +89,7 @@ struct ammon_runtime {
   ammon_rt::Kernels k;
   ammon_device_info info = {};
   uint32_t gemv_wgs_per_cu = 4;
+  int gemm_split = -1;  // prefill GEMM reduction split: -1 by shape, 0 never, 1 always
   std::mutex occ_mu;
   std::map<std::pair<hipFunction_t, size_t>, uint32_t> occ_cache;
 };

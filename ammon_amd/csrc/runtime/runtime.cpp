@@ -138,11 +138,14 @@ static ammon_status load_kernels(ammon_runtime *rt) {
       R(6, name, k.token[d][g]);
     }
   for (int d = 0; d < 2; ++d)
-    for (int m = 0; m < kGemvModes; ++m) {
-      char name[96];
-      snprintf(name, sizeof name, "ammon_gemm_%s_%s", dtn[d], modes[m]);
-      R(7, name, k.gemm[d][m]);
-    }
+    for (int t = 0; t < 2; ++t)
+      for (int s = 0; s < 2; ++s)
+        for (int m = 0; m < kGemvModes; ++m) {
+          char name[96];
+          snprintf(name, sizeof name, "ammon_gemm_%s_%s_t%d%s", dtn[d], modes[m], t ? 32 : 16,
+                   s ? "_k4" : "");
+          R(7, name, k.gemm[d][t][s][m]);
+        }
 #undef R
   return AMMON_OK;
 }
@@ -184,6 +187,10 @@ static ammon_status create(int device, ammon_runtime **out) {
   rt->info.total_memory = prop.totalGlobalMem;
   std::snprintf(rt->info.arch, sizeof rt->info.arch, "%.63s", prop.gcnArchName);
   std::snprintf(rt->info.name, sizeof rt->info.name, "%.127s", prop.name);
+  if (const char *env = std::getenv("AMMON_GEMM_SPLIT")) {
+    const int v = std::atoi(env);
+    if (v == 0 || v == 1) rt->gemm_split = v;
+  }
   if (const char *env = std::getenv("AMMON_GEMV_WGS_PER_CU")) {
     int v = std::atoi(env);
     if (v > 0 && v <= 64) rt->gemv_wgs_per_cu = (uint32_t)v;

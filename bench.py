@@ -220,6 +220,61 @@ def cpu_baseline(rt, model, c, weights, start_pos, token0, gpu_tokens, budget_s)
     }
 
 
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_measure(rt, model, c, prompt_lengths=(16, 512), reps=3):
+    """Prompt prefill (one pass per layer: GEMMs on matrix cores, token-
+    batched attention) of T-token prompts from position 0: whole-model
+    time, and the gate/up GEMM + SwiGLU alone (events around 10 launches on
+    the model's stream).  Short prompts are HBM-bound on W (bytes: W once +
+    x + hb); long ones are matrix-core bound, the bf16 W against x split
+    into three bf16 parts (three MFMAs per product: issued TFLOP/s = 3 x
+    algorithmic)."""
+    from ammon_amd import Timer
+    from ammon_amd._abi import BF16, F32, call
+
+    out = {}
+    timer = Timer(rt)
+    stream = model.stream
+    w1 = ctypes.c_void_p(int(model.weights["w1"]))
+    w3 = ctypes.c_void_p(int(model.weights["w3"]))
+    for T in prompt_lengths:
+        prompt = (np.arange(T) * 7919 % c.vocab).astype(np.int32)
+        model.prefill(prompt)  # warm: scratch allocation, first launches
+        ts = []
+        for _ in range(reps):
+            t0 = time.perf_counter()
+            model.prefill(prompt)  # synchronises
+            ts.append(time.perf_counter() - t0)
+        ms = min(ts) * 1e3
+        x = rt.alloc(T * c.dim * 4)
+        rt.fill_normal(x, F32, T * c.dim, 1, 7)
+        hb = rt.alloc(T * c.hidden * 4)
+        args = (rt.handle, stream, x, T, w1, w3, BF16, c.dim, c.hidden, hb)
+        call("ammon_prefill_gate_up_swiglu", *args)
+        timer.start(stream)
+        for _ in range(10):
+            call("ammon_prefill_gate_up_swiglu", *args)
+        timer.stop(stream)
+        us = timer.elapsed_ms() * 1e3 / 10
+        x.free()
+        hb.free()
+        nbytes = 2 * c.hidden * c.dim * 2 + T * c.dim * 4 + T * c.hidden * 4
+        flops = 2.0 * T * 2 * c.hidden * c.dim
+        gemm = {"kernel": "ammon_gemm_bf16_swiglu (gate/up GEMM + SwiGLU)", "avg_us": round(us, 2),
+                "bytes": nbytes, "gbs": round(nbytes / (us * 1e-6) / 1e9, 1),
+                "hbm_frac": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                "tflops": round(flops / (us * 1e-6) / 1e12, 1),
+                "mfma_frac": round(3 * flops / (us * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)}
+        out[str(T)] = {"tokens": T, "ms": round(ms, 3), "tokens_per_s": round(T / ms * 1e3, 1),
+                       "gate_up_gemm": gemm}
+        log(f"prefill T={T}: {ms:.2f} ms ({T / ms * 1e3:.0f} tok/s); gate/up GEMM {us:.1f} us, "
+            f"{gemm['gbs']:.0f} GB/s, {gemm['tflops']:.1f} TFLOP/s")
+    timer.close()
+    return out
+
+
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
                             "hbm_traffic_llama3_8b_ctx8192.json")
 
@@ -279,6 +334,7 @@ def main():
                     help="one persistent cooperative kernel per token")
     ap.add_argument("--split", type=int, default=0,
                     help="attention split length (0: the library's choice)")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prompt-prefill lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain streaming kernel of known size (ammon_add over "
                          "256 MiB operands), the calibration for HBM byte counters")
@@ -352,6 +408,9 @@ def main():
                            args.cpu_budget)
         log(f"cpu baseline: {cpu}")
 
+    # after the CPU baseline: prefill rewrites the first cache positions
+    prefill = None if args.no_prefill else prefill_measure(rt, model, c)
+
     result = {
         "metric": METRIC,
         "value": round(tps, 3),
@@ -392,6 +451,7 @@ def main():
             "avg_launch_us": dom["avg_us"],
         },
         "kernels": kernels,
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     model.close()

@@ -51,9 +51,13 @@ def pos_major(hm, kv_heads, seq, head):
 
 # ---- GEMM -----------------------------------------------------------------------------------
 # (d, n, tokens): tails in every dimension -- rows past a 64-row tile, n past
-# a 256-wide chunk (288 = 256 + 32), tokens past 16- and 32-token tiles.
+# a 256-wide chunk (288 = 256 + 32), tokens past 16- and 32-token tiles.  The
+# library splits the reduction over a workgroup's waves (16-row tiles) when
+# 64-row tiles would not fill the device; the last two shapes take 64-row
+# tiles (16- and 32-token variants).
 GEMM_SHAPES = [(4096, 4096, 16), (1024, 4096, 33), (288, 288, 8), (768, 288, 40),
-               (288, 768, 7), (100, 264, 5), (5, 8, 3), (64, 256, 1), (130, 4104, 64)]
+               (288, 768, 7), (100, 264, 5), (5, 8, 3), (64, 256, 1), (130, 4104, 64),
+               (32768, 64, 16), (4096, 264, 256)]
 
 
 @pytest.mark.parametrize("d,n,tokens", GEMM_SHAPES)
@@ -98,7 +102,8 @@ def test_prefill_gemm_validation(rt):
 
 
 @pytest.mark.parametrize("dim,hidden,tokens,w_dtype",
-                         [(288, 768, 8, F32), (4096, 14336, 16, BF16), (64, 200, 35, BF16)])
+                         [(288, 768, 8, F32), (4096, 14336, 16, BF16), (64, 200, 35, BF16),
+                          (64, 16400, 16, BF16), (64, 4100, 100, F32)])
 def test_prefill_gate_up_swiglu(rt, dim, hidden, tokens, w_dtype):
     w1 = oracle.storage(oracle.normal(hidden * dim, 211, std=0.02), w_dtype).reshape(hidden, dim)
     w3 = oracle.storage(oracle.normal(hidden * dim, 212, std=0.02), w_dtype).reshape(hidden, dim)
@@ -111,13 +116,15 @@ def test_prefill_gate_up_swiglu(rt, dim, hidden, tokens, w_dtype):
     assert rel_err(hb.download((tokens, hidden)), want) <= RTOL
 
 
-@pytest.mark.parametrize("shape", ["c1", "c4"])
+@pytest.mark.parametrize("shape", ["c1", "c4", "c4_long"])
 @pytest.mark.parametrize("kv_dtype", [F32, BF16])
 def test_prefill_qkv_rope_store(rt, shape, kv_dtype):
     if shape == "c1":
         dim, q_heads, kv_heads, head, seq, w_dtype, theta, p0, T = 288, 6, 6, 48, 64, F32, 1e4, 0, 9
-    else:
+    elif shape == "c4":
         dim, q_heads, kv_heads, head, seq, w_dtype, theta, p0, T = 4096, 32, 8, 128, 96, BF16, 5e5, 30, 40
+    else:  # enough token tiles for 64-row tiles; a narrow model keeps the oracle quick
+        dim, q_heads, kv_heads, head, seq, w_dtype, theta, p0, T = 512, 32, 8, 128, 256, BF16, 5e5, 5, 200
     qd, kd = q_heads * head, kv_heads * head
     wq = oracle.storage(oracle.normal(qd * dim, 221, std=0.02), w_dtype).reshape(qd, dim)
     wk = oracle.storage(oracle.normal(kd * dim, 222, std=0.02), w_dtype).reshape(kd, dim)
