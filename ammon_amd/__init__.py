@@ -14,6 +14,7 @@ from .runtime import (DeviceBuffer, Runtime, Timer, argmax_scratch_bytes, attent
 
 from . import model
 from .model import LlamaModel
+from .tokenizer import BpeTokenizer
 
 LIB_PATH = _abi.LIB_PATH
 
@@ -21,5 +22,5 @@ __all__ = [
     "ATTENTION_MAX_HEAD", "ATTENTION_SPLIT_REF", "BF16", "DEFAULT_ROPE_THETA", "F32",
     "AmmonError", "DecodeStep", "DeviceBuffer", "Runtime", "Timer", "argmax_scratch_bytes",
     "attention_scratch_bytes", "attention_splits", "kv_permute", "kv_unpermute",
-    "rope_table_host", "storage_dtype", "LIB_PATH", "LlamaModel", "model",
+    "rope_table_host", "storage_dtype", "LIB_PATH", "LlamaModel", "model", "BpeTokenizer",
 ]

@@ -149,6 +149,23 @@ SIGNATURES.update({
     "ammon_llama_token_trace": (_ST, [_P, _P, _SZ, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
 })
 
+# include/ammon/ammon_tokenizer.h
+SIGNATURES.update({
+    "ammon_bpe_load": (_ST, [ctypes.c_char_p, _U32, ctypes.POINTER(_P)]),
+    "ammon_bpe_from_parts": (_ST, [ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(_U32),
+                                   ctypes.POINTER(_F), _U32, _U32, ctypes.POINTER(_P)]),
+    "ammon_bpe_destroy": (_ST, [_P]),
+    "ammon_bpe_vocab_size": (_U32, [_P]),
+    "ammon_bpe_max_token_length": (_U32, [_P]),
+    "ammon_bpe_encode": (_ST, [_P, ctypes.c_char_p, _SZ, ctypes.c_int, ctypes.c_int, _P, _SZ,
+                               ctypes.POINTER(_SZ)]),
+    "ammon_bpe_decode": (_ST, [_P, _I32, _I32, _P, _SZ, ctypes.POINTER(_SZ)]),
+    "ammon_llama_generate_text": (_ST, [_P, _P, ctypes.c_char_p, _SZ, _U32, ctypes.c_int,
+                                        ctypes.c_int, ctypes.c_int, _I32, ctypes.c_int, _P, _SZ,
+                                        ctypes.POINTER(_SZ), _P, _U32, ctypes.POINTER(_U32),
+                                        ctypes.POINTER(ctypes.c_double)]),
+})
+
 
 class AmmonError(RuntimeError):
     """A non-OK ammon_status with the library's thread-local message."""

@@ -18,8 +18,11 @@
 #include "../runtime/internal.h"
 #include "ammon/ammon.hpp"
 #include "ammon/ammon_model.h"
+#include "ammon/ammon_tokenizer.h"
 
 namespace ammon {
+
+const BpeTokenizer &bpe_of(const ammon_bpe *t);  // host/tokenizer.cpp
 namespace {
 
 // One cooperative launch per token (kernels/token.hip): the same arithmetic
@@ -770,6 +773,45 @@ ammon_status ammon_llama_generate_tokens_prefill(ammon_llama *m, const int32_t *
     auto o = m->model->generate_prefill(
         p, max_new_tokens, has_stop ? std::optional<int32_t>(stop_on) : std::nullopt, last_logits);
     fill_output(o, out_tokens, n_out, tokens_per_second);
+  });
+}
+
+ammon_status ammon_llama_generate_text(ammon_llama *m, const ammon_bpe *t, const char *prompt,
+                                       size_t prompt_len, uint32_t max_new_tokens, int bos,
+                                       int eos, int has_stop, int32_t stop_on, int loop,
+                                       char *text, size_t text_capacity, size_t *text_len,
+                                       int32_t *tokens, uint32_t token_capacity,
+                                       uint32_t *n_tokens, double *tokens_per_second) {
+  AMMON_CHECK(m && t && text_len && n_tokens && (prompt || prompt_len == 0) &&
+                  (text || text_capacity == 0) && (tokens || token_capacity == 0),
+              "llama_generate_text: NULL argument");
+  AMMON_CHECK(loop >= 0 && loop <= 2, "llama_generate_text: loop must be 0, 1 or 2");
+  return guarded([&] {
+    const ammon::BpeTokenizer &tok = ammon::bpe_of(t);
+    const std::vector<int32_t> ids =
+        tok.encode(std::string(prompt ? prompt : "", prompt_len), bos != 0, eos != 0);
+    if (ids.empty()) throw ammon::Error(AMMON_E_VALIDATION, "expected at least one prompt token");
+    for (int32_t id : ids)
+      if (id < 0 || (size_t)id >= m->model->vocab_size())
+        throw ammon::Error(AMMON_E_VALIDATION, "prompt token " + std::to_string(id) +
+                                                   " outside the model's vocab");
+    const std::optional<int32_t> stop = has_stop ? std::optional<int32_t>(stop_on) : std::nullopt;
+    const ammon::GenerateTokenOutput o =
+        loop == 0 ? ammon::generate_tokens(*m->model, ids, max_new_tokens, stop)
+        : loop == 1 ? m->model->generate_device(ids, max_new_tokens, stop, nullptr)
+                    : m->model->generate_prefill(ids, max_new_tokens, stop, nullptr);
+    const std::string s = ammon::decode_tokens(tok, ids[0], o.tokens);
+    if (text_capacity) {
+      const size_t k = std::min(text_capacity - 1, s.size());
+      std::memcpy(text, s.data(), k);
+      text[k] = '\0';
+    }
+    *text_len = s.size();
+    std::copy(o.tokens.begin(),
+              o.tokens.begin() + (ptrdiff_t)std::min<size_t>(token_capacity, o.tokens.size()),
+              tokens);
+    *n_tokens = (uint32_t)o.tokens.size();
+    if (tokens_per_second) *tokens_per_second = o.tokens_per_second;
   });
 }
 

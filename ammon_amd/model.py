@@ -124,6 +124,26 @@ class LlamaModel:
         return self._generate("ammon_llama_generate_tokens_prefill", prompt, max_new_tokens,
                               stop_on)
 
+    def generate_text(self, tokenizer, prompt: str, max_new_tokens: int = 50, bos: bool = True,
+                      eos: bool = False, stop_on=None, loop: str = "host"):
+        """The reference's generate (src/generate.rs:93-118): (text, tokens,
+        tok/s).  loop: "host" (argmax on the host per step, the reference's
+        loop), "device" (device greedy loop) or "prefill" (one-pass prompt
+        prefill, then the device loop)."""
+        modes = {"host": 0, "device": 1, "prefill": 2}
+        data = prompt.encode()
+        cap = 1 << 16
+        text = ctypes.create_string_buffer(cap)
+        tokens = np.empty(max(int(max_new_tokens), 1), np.int32)
+        tlen, n, tps = ctypes.c_size_t(), ctypes.c_uint32(), ctypes.c_double()
+        call("ammon_llama_generate_text", self.handle, tokenizer.handle, data, len(data),
+             max_new_tokens, int(bos), int(eos), int(stop_on is not None), int(stop_on or 0),
+             modes[loop], text, cap, ctypes.byref(tlen), tokens.ctypes.data, tokens.size,
+             ctypes.byref(n), ctypes.byref(tps))
+        if tlen.value >= cap:
+            raise RuntimeError("generated text exceeds the 64 KiB buffer")
+        return text.raw[: tlen.value].decode(), tokens[: n.value].copy(), tps.value
+
     def prefill(self, tokens, start_pos: int = 0) -> np.ndarray:
         """Run tokens at positions start_pos.. in one pass; the last
         position's logits."""

@@ -385,4 +385,67 @@ GenerateTokenOutput generate_tokens(AutoregressiveModel &model,
                                     uint32_t max_new_tokens,
                                     std::optional<int32_t> stop_on = std::nullopt);
 
+// ---- tokenizer and text generation ------------------------------------------------------
+// String <-> token ids (src/tokenizer.rs:11-16).  Strings are UTF-8 bytes.
+class Tokenizer {
+ public:
+  virtual ~Tokenizer() = default;
+  virtual size_t vocab_size() const = 0;
+  virtual std::vector<int32_t> encode(const std::string &text, bool bos, bool eos) const = 0;
+  virtual std::string decode(int32_t prev_token, int32_t token) const = 0;
+};
+
+// SentencePiece-style BPE over a llama2.c tokenizer.bin (src/tokenizer.rs:
+// 18-177): pieces, merge scores, dummy-prefix encoding with byte fallback
+// (byte b -> id b + 3) and greedy highest-score pair merging.
+class BpeTokenizer : public Tokenizer {
+ public:
+  // tokenizer.bin: u32 max_token_length, then per piece f32 score, i32
+  // length, bytes (pieces are read as UTF-8 with invalid sequences replaced
+  // by U+FFFD, as the reference's from_utf8_lossy).
+  static BpeTokenizer from_path(const std::string &path, size_t vocab_size);
+  static BpeTokenizer from_parts(std::vector<std::string> vocab, std::vector<float> scores,
+                                 uint32_t max_token_length);
+  uint32_t max_token_length() const { return max_token_length_; }
+  static int32_t bos_id() { return 1; }
+  static int32_t eos_id() { return 2; }
+
+  size_t vocab_size() const override { return vocab_.size(); }
+  std::vector<int32_t> encode(const std::string &text, bool bos, bool eos) const override;
+  std::string decode(int32_t prev_token, int32_t token) const override;
+  const std::string &piece(int32_t id) const { return vocab_.at((size_t)id); }
+
+ private:
+  int32_t lookup(const std::string &s) const;  // -1 when absent
+  std::vector<std::string> vocab_;
+  std::vector<float> scores_;
+  uint32_t max_token_length_ = 0;
+  std::vector<std::pair<std::string, int32_t>> sorted_;
+};
+
+struct GenerateOptions {  // src/generate.rs:8-26
+  uint32_t max_new_tokens = 50;
+  bool bos = true;
+  bool eos = false;
+  std::optional<int32_t> stop_on;  // stop when chosen after the prompt
+};
+
+struct GenerateOutput {  // src/generate.rs:35-41
+  std::string text;
+  std::vector<int32_t> tokens;
+  size_t prompt_tokens = 0;
+  double tokens_per_second = 0.0;
+};
+
+// Text of a token sequence as the reference's generate assembles it
+// (src/generate.rs:106-113): decode(prev, token) with prev starting at
+// `first`.
+std::string decode_tokens(const Tokenizer &tokenizer, int32_t first,
+                          const std::vector<int32_t> &tokens);
+
+// The reference's text generation (src/generate.rs:93-118): encode the
+// prompt, run generate_tokens, decode the tokens after the first prompt token.
+GenerateOutput generate(AutoregressiveModel &model, const Tokenizer &tokenizer,
+                        const std::string &prompt, const GenerateOptions &options = {});
+
 }  // namespace ammon
