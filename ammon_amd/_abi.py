@@ -149,6 +149,17 @@ SIGNATURES.update({
     "ammon_llama_token_trace": (_ST, [_P, _P, _SZ, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
 })
 
+# include/ammon/ammon_checkpoint.h
+SIGNATURES.update({
+    "ammon_checkpoint_probe": (_ST, [ctypes.c_char_p, ctypes.POINTER(LlamaConfig),
+                                     ctypes.POINTER(_U32), ctypes.POINTER(_U32),
+                                     ctypes.POINTER(_U64)]),
+    "ammon_checkpoint_load": (_ST, [_P, ctypes.c_char_p, _DT, ctypes.POINTER(_P)]),
+    "ammon_checkpoint_config": (_ST, [_P, ctypes.POINTER(LlamaConfig)]),
+    "ammon_checkpoint_weights": (_ST, [_P, ctypes.POINTER(LlamaWeights)]),
+    "ammon_checkpoint_free": (_ST, [_P]),
+})
+
 # include/ammon/ammon_tokenizer.h
 SIGNATURES.update({
     "ammon_bpe_load": (_ST, [ctypes.c_char_p, _U32, ctypes.POINTER(_P)]),

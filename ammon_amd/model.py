@@ -38,6 +38,55 @@ def weight_dtype(cfg, name: str) -> int:
     return F32 if name.startswith("rms") else cfg.w_dtype
 
 
+class CheckpointConfig:
+    """A model shape read from a checkpoint header (attributes as the C
+    config's fields)."""
+
+    def __init__(self, c):
+        for name, _ in _abi.LlamaConfig._fields_:
+            setattr(self, name, getattr(c, name))
+
+
+def probe_checkpoint(path: str):
+    """(CheckpointConfig, layout 0 legacy / 1 version 1, shared classifier,
+    expected file bytes) from the header alone (no device)."""
+    c, fmt, shared, size = _abi.LlamaConfig(), ctypes.c_uint32(), ctypes.c_uint32(), ctypes.c_uint64()
+    call("ammon_checkpoint_probe", str(path).encode(), ctypes.byref(c), ctypes.byref(fmt),
+         ctypes.byref(shared), ctypes.byref(size))
+    return CheckpointConfig(c), fmt.value, bool(shared.value), size.value
+
+
+class Checkpoint:
+    """Device weights loaded by ammon_checkpoint_load."""
+
+    def __init__(self, rt: Runtime, path: str, w_dtype: int = F32):
+        self.rt = rt
+        h = ctypes.c_void_p()
+        call("ammon_checkpoint_load", rt.handle, str(path).encode(), w_dtype, ctypes.byref(h))
+        self.handle = h
+
+    def config(self) -> CheckpointConfig:
+        c = _abi.LlamaConfig()
+        call("ammon_checkpoint_config", self.handle, ctypes.byref(c))
+        return CheckpointConfig(c)
+
+    def weights(self) -> dict:
+        w = _abi.LlamaWeights()
+        call("ammon_checkpoint_weights", self.handle, ctypes.byref(w))
+        return {n: getattr(w, n) for n in WEIGHT_NAMES}
+
+    def close(self) -> None:
+        if self.handle:
+            call("ammon_checkpoint_free", self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
 class LlamaModel:
     """A device model over caller-owned device weights.
 
@@ -80,6 +129,24 @@ class LlamaModel:
             dev[name] = buf
         rt.synchronize()
         return cls(rt, cfg, dev, **kw)
+
+    @classmethod
+    def from_checkpoint(cls, rt: Runtime, path: str, w_dtype: int = F32, kv_dtype: int = None,
+                        max_seq: int = None, theta: float = None, **kw) -> "LlamaModel":
+        """A llama2.c checkpoint (legacy or version-1 layout) loaded onto the
+        device in w_dtype; the shape comes from its header (max_seq and theta
+        may be overridden: the file carries neither theta nor a KV budget)."""
+        ck = Checkpoint(rt, path, w_dtype)
+        cfg = ck.config()
+        if kv_dtype is not None:
+            cfg.kv_dtype = kv_dtype
+        if max_seq is not None:
+            cfg.max_seq = max_seq
+        if theta is not None:
+            cfg.theta = theta
+        m = cls(rt, cfg, ck.weights(), **kw)
+        m.checkpoint = ck  # keeps the device weights alive
+        return m
 
     def close(self) -> None:
         if self.handle:
