@@ -226,12 +226,24 @@ struct AttnPartial {
       }
     };
 
-    for (uint32_t c0 = 0; c0 < n; c0 += 2 * chunk) {
+    // Steady state: both buffers are refilled two chunks ahead.  The last
+    // (at most three) chunks run without prefetches: a load past the split
+    // would return only zeros, but the merge below reuses its registers and
+    // would first wait for it to come back.
+    uint32_t c0 = 0;
+    for (; c0 + 3 * chunk < n; c0 += 2 * chunk) {
       compute_chunk(c0, kA, vA);
       load_chunk(c0 + 2 * chunk, kA, vA);
-      if (c0 + chunk >= n) break;
       compute_chunk(c0 + chunk, kB, vB);
       load_chunk(c0 + 3 * chunk, kB, vB);
+    }
+    if (c0 < n) {
+      compute_chunk(c0, kA, vA);
+      if (c0 + 2 * chunk < n) load_chunk(c0 + 2 * chunk, kA, vA);
+      if (c0 + chunk < n) {
+        compute_chunk(c0 + chunk, kB, vB);
+        if (c0 + 2 * chunk < n) compute_chunk(c0 + 2 * chunk, kA, vA);
+      }
     }
 
     // merge the 4 * PW slots of the workgroup through LDS
@@ -446,20 +458,30 @@ struct AttnPartialMfma {
       }
     };
 
-    // buffers keep fixed roles (unrolled); each is refilled NBUF chunks ahead
-    for (uint32_t c0 = 0; c0 < n; c0 += NBUF * CHUNK) {
-      bool more = true;
+    // Buffers keep fixed roles (unrolled); each is refilled NBUF chunks
+    // ahead.  Steady state while every refill lies inside the split; the
+    // last 2 NBUF - 1 chunks at most run in two passes, the second without
+    // prefetches: a load past the split returns only zeros, but the merge
+    // below reuses its registers and would first wait for it to come back.
+    const uint32_t nch = (n + CHUNK - 1) / CHUNK;
+    uint32_t c = 0;  // chunk index
+    for (; c + 2 * NBUF <= nch; c += NBUF) {
 #pragma unroll
       for (int b = 0; b < NBUF; ++b) {
-        const uint32_t c = c0 + b * CHUNK;
-        if (more && c < n) {
-          process(c, kb[b], vb[b]);
-          load_chunk(c + NBUF * CHUNK, kb[b], vb[b]);
-        } else {
-          more = false;
-        }
+        process((c + b) * CHUNK, kb[b], vb[b]);
+        load_chunk((c + b + NBUF) * CHUNK, kb[b], vb[b]);
       }
     }
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) {
+      if (c + b < nch) {
+        process((c + b) * CHUNK, kb[b], vb[b]);
+        if (c + b + NBUF < nch) load_chunk((c + b + NBUF) * CHUNK, kb[b], vb[b]);
+      }
+    }
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b)
+      if (c + NBUF + b < nch) process((c + NBUF + b) * CHUNK, kb[b], vb[b]);
 
     // merge: plain sums over the 16 position slots (4 per wave) of the group
     __syncthreads();
