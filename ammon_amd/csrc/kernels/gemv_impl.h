@@ -382,27 +382,46 @@ struct GemvPass {
 
     // Two-stage pipeline: compute one buffer, then refill it with the tile
     // two ahead, so the other buffer's loads stay in flight meanwhile.
-    // Unrolled so each buffer keeps a fixed role.
+    // Unrolled so each buffer keeps a fixed role.  The steady state runs
+    // while both refills are real tiles (loads unconditional, so the wait
+    // counts stay exact); the last one to three tiles run without refills
+    // past the end -- those would return only zeros, yet the wave could not
+    // retire before they came back.
     uint32_t blk2 = blk1, ti2 = ti1;
     advance(blk2, ti2, tiles, nwg);
-    while (blk < p.row_blocks) {
+    auto shift = [&] {
+      blk = blk1;
+      ti = ti1;
+      blk1 = blk2;
+      ti1 = ti2;
+      advance(blk2, ti2, tiles, nwg);
+    };
+    const uint32_t total = (wg < p.row_blocks ? (p.row_blocks - 1 - wg) / nwg + 1 : 0) * tiles;
+    uint32_t i = 0;
+    for (; i + 3 < total; i += 2) {
       compute(ti, bufA);
       if (ti + 1 == tiles) finish(blk);
       load_tile(blk2, ti2, bufA);
-      blk = blk1;
-      ti = ti1;
-      blk1 = blk2;
-      ti1 = ti2;
-      advance(blk2, ti2, tiles, nwg);
-      if (blk >= p.row_blocks) break;
+      shift();
       compute(ti, bufB);
       if (ti + 1 == tiles) finish(blk);
       load_tile(blk2, ti2, bufB);
-      blk = blk1;
-      ti = ti1;
-      blk1 = blk2;
-      ti1 = ti2;
-      advance(blk2, ti2, tiles, nwg);
+      shift();
+    }
+    if (i < total) {
+      compute(ti, bufA);
+      if (ti + 1 == tiles) finish(blk);
+      if (i + 2 < total) load_tile(blk2, ti2, bufA);
+      shift();
+      if (i + 1 < total) {
+        compute(ti, bufB);
+        if (ti + 1 == tiles) finish(blk);
+        shift();
+        if (i + 2 < total) {
+          compute(ti, bufA);
+          if (ti + 1 == tiles) finish(blk);
+        }
+      }
     }
   }
 };
