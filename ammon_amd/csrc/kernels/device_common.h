@@ -31,29 +31,35 @@ AMMON_DEV void store_elem(void *base, uint32_t dtype, size_t i, float v) {
     ((float *)base)[i] = v;
 }
 
-// Output stores at agent scope (global_store ... sc1): written through to
-// the device coherence point, so another XCD that has not cached the line
-// reads the new value without any L2 writeback.  Activations, K/V rows and
-// attention partials are stored this way; every kernel's outputs are small.
-AMMON_DEV void st_out(float *p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+// Output stores (activations, K/V rows, attention partials).  A code object
+// that hands results to other workgroups inside one launch (the persistent
+// token kernel) defines AMMON_AGENT_STORES to 1 before including this
+// header: its outputs are then stored at agent scope (global_store ... sc1),
+// written through to the device coherence point, so another XCD that has
+// not cached the line reads the new value without any L2 writeback.
+// Standalone kernels hand results over at kernel boundaries only and use
+// plain stores, which complete at L2.
+#ifndef AMMON_AGENT_STORES
+#define AMMON_AGENT_STORES 0
+#endif
+template <typename T>
+AMMON_DEV void st_out_t(T *p, T v) {
+  if (AMMON_AGENT_STORES)
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  else
+    *p = v;
 }
-AMMON_DEV void st_out(uint32_t *p, uint32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-AMMON_DEV void st_out(int32_t *p, int32_t v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+AMMON_DEV void st_out(float *p, float v) { st_out_t(p, v); }
+AMMON_DEV void st_out(uint32_t *p, uint32_t v) { st_out_t(p, v); }
+AMMON_DEV void st_out(int32_t *p, int32_t v) { st_out_t(p, v); }
 // Elements i and i + 1 (i even) of an fp32 / bf16 array as one store.
 AMMON_DEV void store_pair_out(void *base, uint32_t dtype, size_t i, float a, float b) {
   if (dtype == AMMON_K_BF16) {
     const uint32_t w = (uint32_t)f32_to_bf16(a) | ((uint32_t)f32_to_bf16(b) << 16);
-    __hip_atomic_store((uint32_t *)((uint16_t *)base + i), w, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    st_out_t((uint32_t *)((uint16_t *)base + i), w);
   } else {
     const uint64_t w = (uint64_t)__float_as_uint(a) | ((uint64_t)__float_as_uint(b) << 32);
-    __hip_atomic_store((uint64_t *)((float *)base + i), w, __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+    st_out_t((uint64_t *)((float *)base + i), w);
   }
 }
 

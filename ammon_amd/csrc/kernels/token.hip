@@ -34,6 +34,8 @@
 // balance without a profiler; the stamps are a few stores per barrier).
 //
 // Requires all gridDim.x workgroups to be co-resident (cooperative launch).
+// outputs cross workgroups within the launch: agent-scope stores
+#define AMMON_AGENT_STORES 1
 #include "argmax_impl.h"
 #include "attention_impl.h"
 #include "gemv_impl.h"
