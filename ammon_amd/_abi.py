@@ -100,6 +100,9 @@ SIGNATURES = {
     "ammon_argmax_scratch_bytes": (_SZ, [_U32]),
     "ammon_argmax": (_ST, [_P, _P, _P, _U32, _P, _P]),
     "ammon_greedy_next": (_ST, [_P, _P, _P, _U32, _P, _P, _U32, _P, _P, _U32]),
+    "ammon_greedy_lm_head_scratch_bytes": (_SZ, [_P]),
+    "ammon_greedy_lm_head": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _DT, _U32, _U32, _P, _P, _SZ,
+                                   _P, _U32, _P, _P, _U32]),
     "ammon_prefill_gemm": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P, _P]),
     "ammon_prefill_qkv_rope_store": (_ST, [_P, _P, _P, _U32, _P, _P, _P, _DT, _U32, _U32, _U32,
                                            _U32, _P, _P, _P, _DT, _U32, _P, _P]),

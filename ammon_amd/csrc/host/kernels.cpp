@@ -289,6 +289,36 @@ void greedy_next(Scheme &s, const std::string &label, TensorView logits, TensorV
   });
 }
 
+void greedy_lm_head(Scheme &s, const std::string &label, TensorView weight, TensorView x,
+                    TensorView norm_weight, TensorView logits, TensorView scratch,
+                    TensorView prompt, uint32_t n_prompt, const Tensor &step, TensorView tokens,
+                    float eps) {
+  const std::string k = "greedy_lm_head";
+  expect_rank(k, weight, "weight", 2);
+  expect_f32(k, x, "x");
+  expect_f32(k, logits, "logits");
+  expect_step(k, step);
+  const uint32_t d = weight.shape().dim(0), n = weight.shape().dim(1);
+  if (x.numel() != n) fail(k + ": parameter `x` must have " + std::to_string(n) + " elements");
+  if (norm_weight.numel() != n)
+    fail(k + ": parameter `norm` must have " + std::to_string(n) + " elements");
+  if (logits.numel() != d) fail(k + ": parameter `logits` must have " + std::to_string(d) + " elements");
+  ammon_runtime *rt = s.runtime().raw();
+  if (scratch.nbytes() < ammon_greedy_lm_head_scratch_bytes(rt)) fail(k + ": scratch too small");
+  if (prompt.numel() < n_prompt) fail(k + ": prompt shorter than n_prompt");
+  ammon_decode_step *st = (ammon_decode_step *)step.data();
+  const uint32_t max_tokens = tokens.numel_u32();
+  const ammon_dtype wd = weight.dtype() == DType::BF16 ? AMMON_BF16 : AMMON_F32;
+  const ammon_dtype nd = norm_weight.dtype() == DType::BF16 ? AMMON_BF16 : AMMON_F32;
+  const size_t scratch_bytes = scratch.nbytes();
+  s.record(label, [=](ammon_stream stream) {
+    return ammon_greedy_lm_head(rt, stream, (const float *)x.data(), norm_weight.data(), nd, eps,
+                                weight.data(), wd, d, n, (float *)logits.data(), scratch.data(),
+                                scratch_bytes, (const int32_t *)prompt.data(), n_prompt, st,
+                                (int32_t *)tokens.data(), max_tokens);
+  });
+}
+
 std::shared_ptr<Tensor> rope_table(const Runtime &rt, float theta, uint32_t head, uint32_t seq) {
   // Shared per (device, theta, head, seq) like the reference's prepared
   // kernels (weak entries; the table is freed with its last user).

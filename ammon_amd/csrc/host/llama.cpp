@@ -240,7 +240,9 @@ class LlamaModel : public AutoregressiveModel {
   const std::vector<float> &last_logits() const { return host_logits_; }
 
  private:
-  void record_token(Scheme &s);
+  // greedy: end with the LM head fused with the greedy step (n_prompt
+  // forced tokens) instead of the plain LM head
+  void record_token(Scheme &s, bool greedy = false, uint32_t n_prompt = 0);
   void ensure_decode_scheme(uint32_t n_prompt);
   void ensure_prefill(uint32_t n);
   const float *rope_table();
@@ -328,8 +330,11 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
   step_ = DecodeStep::parcel(rt);
   prompt_ = Tensor::zeros(rt, Shape::vector(c.max_seq), DType::I32);
   tokens_ = Tensor::zeros(rt, Shape::vector(c.max_seq), DType::I32);
-  scratch_ = Tensor::zeros(rt, Shape::vector((uint32_t)(ammon_argmax_scratch_bytes(c.vocab) / 4)),
-                           DType::F32);
+  scratch_ = Tensor::zeros(
+      rt,
+      Shape::vector((uint32_t)(std::max(ammon_argmax_scratch_bytes(c.vocab),
+                                        ammon_greedy_lm_head_scratch_bytes(rt.raw())) / 4)),
+      DType::F32);
   check(ammon_alloc_host(rt.raw(), sizeof(ammon_decode_step), (void **)&pinned_step_), "llama");
   check(ammon_alloc_host(rt.raw(), sizeof(float) * c.vocab, (void **)&pinned_logits_), "llama");
   host_logits_.resize(c.vocab);
@@ -354,22 +359,25 @@ LlamaModel::~LlamaModel() {
   if (pinned_logits_) ammon_free_host(rt_.raw(), pinned_logits_);
 }
 
-void LlamaModel::record_token(Scheme &s) {
+void LlamaModel::record_token(Scheme &s, bool greedy, uint32_t n_prompt) {
   embed_.record(s, tok_emb_, step_, x_.view());
   for (uint32_t l = 0; l < c_.n_layers; ++l) {
     const std::string layer = "layer" + std::to_string(l);
     attn_.record_group(s, layer + "/attn", x_.view(), attn_w_[l], cache_.layer(l), step_);
     ffn_.record_group(s, layer + "/ffn", x_.view(), ffn_w_[l]);
   }
-  lm_head_.record_normed(s, wcls_, x_.view(), rms_final_, logits_.view(), c_.eps);
+  if (greedy)
+    kernels::greedy_lm_head(s, "greedy_lm_head", wcls_, x_.view(), rms_final_, logits_.view(),
+                            scratch_.view(), prompt_.view(), n_prompt, step_, tokens_.view(),
+                            c_.eps);
+  else
+    lm_head_.record_normed(s, wcls_, x_.view(), rms_final_, logits_.view(), c_.eps);
 }
 
 void LlamaModel::ensure_decode_scheme(uint32_t n_prompt) {
   if (decode_scheme_ && decode_prompt_ == n_prompt) return;
   auto s = std::make_unique<Scheme>(rt_, c_.use_graph != 0, stream_);
-  record_token(*s);
-  kernels::greedy_next(*s, "greedy_next", logits_.view(), scratch_.view(), prompt_.view(), n_prompt,
-                       step_, tokens_.view());
+  record_token(*s, true, n_prompt);
   decode_scheme_ = std::move(s);
   decode_prompt_ = n_prompt;
 }

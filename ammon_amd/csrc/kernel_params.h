@@ -87,7 +87,8 @@ enum {
   AMMON_GEMV_PLAIN = 0,
   AMMON_GEMV_RESIDUAL = 1,
   AMMON_GEMV_SWIGLU = 2,
-  AMMON_GEMV_QKV = 3
+  AMMON_GEMV_QKV = 3,
+  AMMON_GEMV_PLAIN_ARGMAX = 4 /* PLAIN, plus one argmax candidate per workgroup */
 };
 
 typedef struct {
@@ -106,6 +107,8 @@ typedef struct {
   uint32_t norm_dtype;
   float eps;
   uint32_t kv_dim, head, seq, kv_dtype; /* QKV */
+  float *cand_v;            /* PLAIN_ARGMAX: [gridDim.x] (value, index) of the */
+  uint32_t *cand_i;         /* first maximum over the workgroup's rows */
 } ammon_k_gemv;
 
 /* Prefill GEMM family: the GEMV modes over `tokens` rows of x at once

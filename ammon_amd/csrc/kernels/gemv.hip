@@ -16,7 +16,8 @@
   GEMV_KERNEL(PREFIX##_plain, WT, CH, RPW, U, AMMON_GEMV_PLAIN)               \
   GEMV_KERNEL(PREFIX##_residual, WT, CH, RPW, U, AMMON_GEMV_RESIDUAL)         \
   GEMV_KERNEL(PREFIX##_swiglu, WT, CH, RPW, U, AMMON_GEMV_SWIGLU)             \
-  GEMV_KERNEL(PREFIX##_qkv, WT, CH, RPW, U, AMMON_GEMV_QKV)
+  GEMV_KERNEL(PREFIX##_qkv, WT, CH, RPW, U, AMMON_GEMV_QKV)                     \
+  GEMV_KERNEL(PREFIX##_plain_argmax, WT, CH, RPW, U, AMMON_GEMV_PLAIN_ARGMAX)
 
 GEMV_MODES(ammon_gemv_bf16_v, uint16_t, 8, 2, 4)
 GEMV_MODES(ammon_gemv_bf16_s, uint16_t, 1, 2, 4)

@@ -23,6 +23,9 @@
 //   SWIGLU    rows interleave gate (w0) and up (w1): r = 2i -> gate row i,
 //             r = 2i+1 -> up row i; y[i] = silu(gate) * up in the reference's
 //             order (src/kernels.rs:472-475)
+//   PLAIN_ARGMAX  PLAIN, and each workgroup writes the (value, lowest index)
+//             of the maximum over its rows (NaN never wins) to cand_v/cand_i
+//             [wg]: pass 1 of the greedy argmax fused into the LM head
 //   QKV       rows run over [Wq; Wk; Wv]; (2i, 2i+1) pairs of q and k rows are
 //             rotated with the cos/sin table at step->position; q goes to y,
 //             rotated k and raw v go to the head-major caches at that position
@@ -43,6 +46,7 @@
 // standalone kernel bit for bit when the rows are 16-byte aligned.
 #pragma once
 
+#include "argmax_impl.h"
 #include "device_common.h"
 
 template <typename WT, int CH, int RPW, int U, int MODE>
@@ -275,6 +279,8 @@ struct GemvPass {
     float acc[RPW];
 #pragma unroll
     for (int k = 0; k < RPW; ++k) acc[k] = 0.f;
+    float cand_v = 0.f;  // PLAIN_ARGMAX: this lane's best row so far
+    uint32_t cand_i = ARGMAX_NONE;
 
     auto compute = [&](uint32_t ti_, V (&buf)[RPW][U]) {
 #pragma unroll
@@ -320,15 +326,20 @@ struct GemvPass {
       }
 #pragma unroll
       for (int k = 0; k < RPW; ++k) acc[k] = wave_sum(acc[k]);
-      if (MODE == AMMON_GEMV_PLAIN || MODE == AMMON_GEMV_RESIDUAL) {
+      if (MODE == AMMON_GEMV_PLAIN || MODE == AMMON_GEMV_RESIDUAL ||
+          MODE == AMMON_GEMV_PLAIN_ARGMAX) {
 #pragma unroll
         for (int k = 0; k < RPW; ++k) {
           const uint32_t vr = r0 + k;
           if ((uint32_t)k == lane && vr < p.rows) {
-            if (MODE == AMMON_GEMV_RESIDUAL)
+            if (MODE == AMMON_GEMV_RESIDUAL) {
               st_out(p.y + vr, ea[k] + acc[k]);
-            else if (write_ok)
+            } else if (MODE == AMMON_GEMV_PLAIN_ARGMAX) {
+              st_out(p.y + vr, acc[k]);
+              if (acc[k] == acc[k]) cand_merge(cand_v, cand_i, acc[k], vr);
+            } else if (write_ok) {
               st_out(yout + vr, acc[k]);
+            }
           }
         }
       } else if (MODE == AMMON_GEMV_SWIGLU) {
@@ -421,6 +432,17 @@ struct GemvPass {
           compute(ti, bufA);
           if (ti + 1 == tiles) finish(blk);
         }
+      }
+    }
+    if (MODE == AMMON_GEMV_PLAIN_ARGMAX) {
+      // the workgroup's candidate; x's LDS is free once every wave is done
+      __syncthreads();
+      float *sv = xs;
+      uint32_t *si = (uint32_t *)(xs + AMMON_WG);
+      block_cand_reduce(cand_v, cand_i, sv, si);
+      if (threadIdx.x == 0) {
+        st_out(p.cand_v + wg, cand_v);
+        st_out(p.cand_i + wg, cand_i);
       }
     }
   }

@@ -32,6 +32,7 @@ struct Kernels {
   hipFunction_t att_partial_h128[2][kAttGroups] = {};
   hipFunction_t att_combine = nullptr;
   hipFunction_t gemv[2][2][kGemvModes] = {};
+  hipFunction_t gemv_argmax[2][2] = {};  // PLAIN_ARGMAX: [dtype][vector?]
   hipFunction_t swiglu = nullptr;
   hipFunction_t add = nullptr;
   hipFunction_t argmax_partial = nullptr;

@@ -74,10 +74,15 @@ struct GemvArgs {
   const float *table;
   uint32_t kv_dim, head, seq;
   ammon_dtype kv_dtype;
+  float *cand_v;       // PLAIN_ARGMAX: candidate arrays of cand_cap entries
+  uint32_t *cand_i;
+  uint32_t cand_cap;
 };
 
+// Validates, packs and launches a GEMV; *grid_out (optional) receives the
+// workgroup count (PLAIN_ARGMAX writes one candidate per workgroup).
 ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemvArgs &a,
-                                   const char *what) {
+                                   const char *what, uint32_t *grid_out = nullptr) {
   AMMON_CHECK(valid_dtype(a.w_dtype), "%s: unknown weight dtype %d", what, (int)a.w_dtype);
   AMMON_CHECK(a.w0 && a.x && a.y, "%s: NULL weight, x or y", what);
   AMMON_CHECK(a.n > 0 && a.d > 0, "%s: empty matrix (d=%u, n=%u)", what, a.d, a.n);
@@ -125,15 +130,21 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   p.head = a.head;
   p.seq = a.seq;
   p.kv_dtype = (uint32_t)a.kv_dtype;
+  p.cand_v = a.cand_v;
+  p.cand_i = a.cand_i;
 
   const int dt = bf ? 1 : 0;
   const int vec = vec_ok;
+  size_t lds = shmem;
+  // PLAIN_ARGMAX reduces the workgroup's candidates in x's LDS
+  if (a.mode == AMMON_GEMV_PLAIN_ARGMAX) lds = std::max<size_t>(lds, 2 * kWorkgroup * 4);
   // Grid: at most gemv_wgs_per_cu resident workgroups per CU (fewer if LDS
   // bounds it); among 2..max per CU pick the count whose grid-stride split of
   // the row blocks wastes the least (blocks / (grid * blocks per workgroup)).
   const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
-  hipFunction_t fn = rt->k.gemv[dt][vec][a.mode];
-  const uint32_t resident = occupancy(rt, fn, shmem);
+  hipFunction_t fn = a.mode == AMMON_GEMV_PLAIN_ARGMAX ? rt->k.gemv_argmax[dt][vec]
+                                                      : rt->k.gemv[dt][vec][a.mode];
+  const uint32_t resident = occupancy(rt, fn, lds);
   const uint32_t max_per_cu = std::max<uint32_t>(1, std::min(rt->gemv_wgs_per_cu, resident));
   uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * max_per_cu);
   double best = -1.0;
@@ -147,7 +158,11 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     }
     if (w == 1 || w <= max_per_cu / 2) break;
   }
-  return launch(rt, stream, fn, grid, 1, (uint32_t)shmem, p, what);
+  if (a.mode == AMMON_GEMV_PLAIN_ARGMAX)
+    AMMON_CHECK(grid <= a.cand_cap, "%s: scratch holds %u candidates, the launch needs %u", what,
+                a.cand_cap, grid);
+  if (grid_out) *grid_out = grid;
+  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
 }
 
 // ---- attention ------------------------------------------------------------------
@@ -761,6 +776,55 @@ ammon_status ammon_argmax(ammon_runtime *rt, ammon_stream stream, const float *l
   AMMON_CHECK(out != nullptr, "argmax: parameter `out` is NULL");
   return argmax_impl(rt, stream, logits, n, scratch, out, nullptr, 0, nullptr, nullptr, 0,
                      "argmax");
+}
+
+size_t ammon_greedy_lm_head_scratch_bytes(ammon_runtime *rt) {
+  if (!rt) return 0;
+  return (size_t)std::max(rt->info.compute_units, 1) * rt->gemv_wgs_per_cu * 8;
+}
+
+ammon_status ammon_greedy_lm_head(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                  const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                  const void *w, ammon_dtype w_dtype, uint32_t vocab,
+                                  uint32_t dim, float *logits, void *scratch,
+                                  size_t scratch_bytes, const int32_t *prompt, uint32_t n_prompt,
+                                  ammon_decode_step *step, int32_t *tokens, uint32_t max_tokens) {
+  REQUIRE_RT();
+  AMMON_CHECK(norm_weight && scratch && step, "greedy_lm_head: NULL norm weight, scratch or step");
+  AMMON_CHECK(n_prompt == 0 || prompt != nullptr, "greedy_lm_head: NULL prompt");
+  AMMON_CHECK(scratch_bytes >= ammon_greedy_lm_head_scratch_bytes(rt),
+              "greedy_lm_head: scratch must be %zu bytes", ammon_greedy_lm_head_scratch_bytes(rt));
+  const uint32_t cap = (uint32_t)std::min<size_t>(scratch_bytes / 8, 0xffffffffu);
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_PLAIN_ARGMAX;
+  a.w0 = w;
+  a.w_dtype = w_dtype;
+  a.d = vocab;
+  a.n = dim;
+  a.rows = vocab;
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = logits;
+  a.cand_v = (float *)scratch;
+  a.cand_i = (uint32_t *)((char *)scratch + (size_t)cap * 4);
+  a.cand_cap = cap;
+  uint32_t grid = 0;
+  ammon_status st = gemv_check_and_launch(rt, stream, a, "greedy_lm_head", &grid);
+  if (st != AMMON_OK || stream == AMMON_STREAM_VALIDATE) return st;
+  ammon_k_argmax p = {};
+  p.logits = logits;
+  p.cand_v = a.cand_v;
+  p.cand_i = a.cand_i;
+  p.step = (ammon_k_step *)step;
+  p.prompt = prompt;
+  p.tokens = tokens;
+  p.n = vocab;
+  p.blocks = grid;
+  p.n_prompt = n_prompt;
+  p.max_tokens = max_tokens;
+  return launch(rt, stream, rt->k.argmax_final, 1, 1, 0, p, "greedy_lm_head");
 }
 
 ammon_status ammon_greedy_next(ammon_runtime *rt, ammon_stream stream, const float *logits,

@@ -125,6 +125,12 @@ static ammon_status load_kernels(ammon_runtime *rt) {
         snprintf(name, sizeof name, "ammon_gemv_%s_%s_%s", dtn[d], v ? "v" : "s", modes[m]);
         R(4, name, k.gemv[d][v][m]);
       }
+  for (int d = 0; d < 2; ++d)
+    for (int v = 0; v < 2; ++v) {
+      char name[96];
+      snprintf(name, sizeof name, "ammon_gemv_%s_%s_plain_argmax", dtn[d], v ? "v" : "s");
+      R(4, name, k.gemv_argmax[d][v]);
+    }
   R(5, "ammon_swiglu", k.swiglu);
   R(5, "ammon_add", k.add);
   R(5, "ammon_argmax_partial", k.argmax_partial);

@@ -287,6 +287,18 @@ ammon_status ammon_greedy_next(ammon_runtime *rt, ammon_stream stream, const flo
                                uint32_t n_prompt, ammon_decode_step *step, int32_t *tokens,
                                uint32_t max_tokens);
 
+/* Final norm + LM head (ammon_gemv_rmsnorm into `logits`) fused with the
+ * first pass of ammon_greedy_next, then its second pass: the same logits,
+ * argmax and DecodeStep update as the two calls, with one launch fewer.
+ * `scratch` holds ammon_greedy_lm_head_scratch_bytes(rt) bytes. */
+size_t ammon_greedy_lm_head_scratch_bytes(ammon_runtime *rt);
+ammon_status ammon_greedy_lm_head(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                  const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                  const void *w, ammon_dtype w_dtype, uint32_t vocab,
+                                  uint32_t dim, float *logits, void *scratch,
+                                  size_t scratch_bytes, const int32_t *prompt, uint32_t n_prompt,
+                                  ammon_decode_step *step, int32_t *tokens, uint32_t max_tokens);
+
 /* ---- prompt prefill -------------------------------------------------------
  * No counterpart kernels in the reference, which feeds a prompt one decode
  * step per token (src/generate.rs:62-64).  These run `tokens` consecutive

@@ -227,6 +227,13 @@ void argmax(Scheme &s, const std::string &label, TensorView logits, TensorView s
             TensorView out);
 void greedy_next(Scheme &s, const std::string &label, TensorView logits, TensorView scratch,
                  TensorView prompt, uint32_t n_prompt, const Tensor &step, TensorView tokens);
+// Final norm + LM head fused with the greedy step (ammon_greedy_lm_head):
+// logits = W rmsnorm(x), then the argmax / prompt forcing / DecodeStep
+// update of greedy_next.
+void greedy_lm_head(Scheme &s, const std::string &label, TensorView weight, TensorView x,
+                    TensorView norm_weight, TensorView logits, TensorView scratch,
+                    TensorView prompt, uint32_t n_prompt, const Tensor &step, TensorView tokens,
+                    float eps);
 // Host cos/sin table for RoPE with the reference's fp32 formula, cached per
 // (device, theta, head, seq) and shared by every block that asks for it.
 std::shared_ptr<Tensor> rope_table(const Runtime &rt, float theta, uint32_t head, uint32_t seq);

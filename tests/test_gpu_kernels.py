@@ -562,3 +562,61 @@ def test_fill_const(rt):
     np.testing.assert_array_equal(down(buf, 1000), 2.5)
     rt.fill(buf, BF16, 1000, 1.0)
     np.testing.assert_array_equal(down(buf, 1000, np.uint16), 0x3F80)
+
+
+@pytest.mark.parametrize("vocab,dim,w_dtype", [(32000, 288, F32), (128256, 512, BF16)])
+def test_greedy_lm_head_matches_unfused(rt, vocab, dim, w_dtype):
+    """The LM head with the argmax folded into it gives the logits of
+    ammon_gemv_rmsnorm bit for bit and the token of ammon_greedy_next on
+    them, with ties (duplicated rows) and NaN rows in play."""
+    wh = oracle.storage(oracle.normal(vocab * dim, 141, std=0.05), w_dtype).reshape(vocab, dim)
+    gh = 1.0 + 0.1 * oracle.normal(dim, 142)
+    xh = oracle.normal(dim, 143)
+    top = int(np.argmax(oracle.gemv(wh, w_dtype, oracle.rmsnorm(xh, gh).reshape(-1))))
+    for idx in (vocab - 3, 70, vocab // 2 + 1):  # copies of the winning row
+        wh[idx] = wh[top]
+    nan = 0x7FC0 if w_dtype == BF16 else np.nan  # bf16 rows hold raw bits
+    wh[11] = nan  # a NaN logit never wins
+    w, g, x = up(rt, wh), up(rt, gh), up(rt, xh)
+    ref, fused = rt.alloc(vocab * 4), rt.alloc(vocab * 4)
+    scratch = rt.alloc(max(_abi.lib.ammon_argmax_scratch_bytes(vocab),
+                           _abi.lib.ammon_greedy_lm_head_scratch_bytes(rt.handle)))
+    prompt = up(rt, np.array([5, 6], np.int32))
+    tok_ref, tok_fused = up(rt, np.full(6, -1, np.int32)), up(rt, np.full(6, -1, np.int32))
+    s_ref, s_fused = rt.step(5, 0), rt.step(5, 0)
+    for i in range(4):
+        call("ammon_gemv_rmsnorm", rt.handle, None, x, g, F32, 1e-5, w, w_dtype, vocab, dim, ref)
+        call("ammon_greedy_next", rt.handle, None, ref, vocab, scratch, prompt, 2, s_ref,
+             tok_ref, 6)
+        call("ammon_greedy_lm_head", rt.handle, None, x, g, F32, 1e-5, w, w_dtype, vocab, dim,
+             fused, scratch, _abi.lib.ammon_greedy_lm_head_scratch_bytes(rt.handle), prompt, 2,
+             s_fused, tok_fused, 6)
+        lr, lf = down(ref, vocab), down(fused, vocab)
+        np.testing.assert_array_equal(lf.view(np.uint32), lr.view(np.uint32))
+        assert rt.read_step(s_fused) == rt.read_step(s_ref)
+        if i >= 1:  # past the forced prompt token
+            assert rt.read_step(s_fused)[0] == oracle.sample_argmax(lf)
+    got = down(tok_fused, 6, np.int32)
+    np.testing.assert_array_equal(got, down(tok_ref, 6, np.int32))
+    assert got[0] == 6 and got[4] == -1
+    lr = down(ref, vocab)
+    if lr[70] == lr[top]:  # bitwise tie between copies: the lowest index wins
+        assert got[1] == min(70, top)
+    # logits[0] NaN: the reference's comparison keeps index 0
+    wh[0] = nan
+    w.upload(wh)
+    call("ammon_greedy_lm_head", rt.handle, None, x, g, F32, 1e-5, w, w_dtype, vocab, dim, fused,
+         scratch, _abi.lib.ammon_greedy_lm_head_scratch_bytes(rt.handle), prompt, 2, s_fused,
+         tok_fused, 6)
+    assert rt.read_step(s_fused)[0] == 0
+
+
+def test_greedy_lm_head_validation(rt):
+    n = _abi.lib.ammon_greedy_lm_head_scratch_bytes(rt.handle)
+    assert n > 0 and n % 8 == 0
+    w, g, x, y = rt.alloc(64 * 64 * 4), rt.alloc(64 * 4), rt.alloc(64 * 4), rt.alloc(64 * 4)
+    scratch, prompt, tokens = rt.alloc(n), rt.alloc(4), rt.alloc(16)
+    step = rt.step(0, 0)
+    with pytest.raises(AmmonError, match="scratch"):
+        call("ammon_greedy_lm_head", rt.handle, None, x, g, F32, 1e-5, w, F32, 64, 64, y,
+             scratch, 8, prompt, 1, step, tokens, 4)
