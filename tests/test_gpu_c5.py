@@ -1,0 +1,87 @@
+"""One Llama-3-70B-shaped decoder layer plus LM head (dim 8192, 64 query /
+8 KV heads of 128, SwiGLU hidden 28672, vocab 128256; bf16 weights and KV
+cache) decoding at context 32768 with the cache prefilled N(0, 1): the
+device path against the oracle on the very same weights and cache.
+
+Weights and cache are generated on the device and copied to the host, so
+both sides start bit-identical.  Logits and the K/V rows the steps write
+must agree to the bf16 bar (a last-bit difference of the fp32 projection
+can flip one bf16 rounding of a cached K/V element), and the greedy token of
+every step must be the oracle's.
+"""
+import ctypes
+
+import numpy as np
+import pytest
+
+import oracle
+from ammon_amd import LlamaModel, kv_unpermute
+from ammon_amd._abi import BF16, F32, call
+
+pytestmark = pytest.mark.gpu
+BF16_TOL = 2e-2
+
+C5 = dict(dim=8192, n_layers=1, n_heads=64, n_kv_heads=8, hidden=28672, vocab=128256,
+          max_seq=32768, theta=500000.0)
+
+
+def rel_err(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    return float(np.max(np.abs(got - want)) / max(np.max(np.abs(want)), 1e-30))
+
+
+def say(msg):
+    print(f"[c5] {msg}", flush=True)
+
+
+def test_c5_layer_decode_at_ctx_32768(rt):
+    cfg = oracle.LlamaConfig(**C5, w_dtype=BF16, kv_dtype=BF16)
+    head = cfg.dim // cfg.n_heads
+    m = LlamaModel.synthetic(rt, cfg, seed=70, std=0.02)
+    for i, name in enumerate(("rms_att", "rms_ffn", "rms_final")):
+        rt.fill_normal(m.weights[name], F32, cfg.dim, 71, i, 1.0, 0.2)
+    kv_n = cfg.n_kv_heads * cfg.max_seq * head
+    k, v = ctypes.c_void_p(), ctypes.c_void_p()
+    call("ammon_llama_kv_layer", m.handle, 0, ctypes.byref(k), ctypes.byref(v))
+    rt.fill_normal(k, BF16, kv_n, 72, 0)
+    rt.fill_normal(v, BF16, kv_n, 72, 1)
+    rt.synchronize()
+    say("weights and cache generated on the device; copying to the host")
+
+    shapes = oracle.weight_shapes(cfg)
+    host = {}
+    for name, buf in m.weights.items():
+        dt = np.float32 if name.startswith("rms") else np.uint16
+        host[name] = buf.download(buf.nbytes // np.dtype(dt).itemsize, dt).reshape(shapes[name])
+    om = oracle.Model(cfg, host)
+    caches = []
+    for src, get in ((k, oracle._lib.orc_model_key_cache), (v, oracle._lib.orc_model_value_cache)):
+        hm = np.empty(kv_n, np.uint16)
+        call("ammon_memcpy", rt.handle, hm.ctypes.data, src, hm.nbytes, 2, None)
+        rt.synchronize()
+        pm = kv_unpermute(hm.reshape(cfg.n_kv_heads, cfg.max_seq, head), cfg.n_kv_heads,
+                          cfg.max_seq, head)
+        ctypes.memmove(get(om._handle, 0), pm.ctypes.data, pm.nbytes)
+        caches.append(pm)
+    say("oracle loaded; decoding")
+
+    tok = 128000
+    for pos in (32765, 32766, 32767):
+        got = m.step(tok, pos)
+        want = om.step(tok, pos)
+        err = rel_err(got, want)
+        say(f"pos {pos}: logits rel err {err:.2e}")
+        assert err <= BF16_TOL, pos
+        assert np.all(np.isfinite(got))
+        nxt = oracle.sample_argmax(want)
+        assert oracle.sample_argmax(got) == nxt, pos
+        tok = nxt
+    # the K/V rows these steps wrote; every other row untouched
+    for got_pm, want_pm, before in zip(m.kv_layer(0), om.kv_layer(0), caches):
+        rows = slice(32765, 32768)
+        assert rel_err(oracle.widen(got_pm[rows], BF16), oracle.widen(want_pm[rows], BF16)) \
+            <= BF16_TOL
+        np.testing.assert_array_equal(got_pm[:32765], before[:32765])
+    om.close()
+    m.close()
