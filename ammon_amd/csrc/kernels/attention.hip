@@ -54,3 +54,12 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine(a
   __shared__ float lds[COMB_LDS_FLOATS];
   attention_combine_unit(attention_token(p, blockIdx.z), blockIdx.x, blockIdx.y, lds);
 }
+
+// Pass 2 for many query tokens: grid (ceil(q_heads / 4), 1, tokens), one
+// wave per (token, q head); the same arithmetic as ammon_attention_combine.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine_waves(
+    ammon_k_attention p) {
+  const ammon_k_attention t = attention_token(p, blockIdx.z);
+  const uint32_t h = blockIdx.x * AMMON_WAVES + (threadIdx.x >> 6);
+  if (h < t.q_heads) attention_combine_wave(t, h);
+}

@@ -527,14 +527,25 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
   return t;
 }
 
-// Pass 2: units (q head, head / 32 dim slices).  Lane (split lane sl, dim
-// quarter) covers splits sl, sl + 64, ...; with up to COMB_ROUNDS * 64 live
-// splits it loads each split's max, sum and 8 of the slice's dims in one
-// round trip and keeps them in registers while the workgroup max M forms
-// (more splits take a second pass over the buffer).  Each split's weight is
-// e^{m_s - M}; the weighted dims and sums are reduced over the splits in
-// LDS, in the same order either way.  Every workgroup of a head computes the
-// same M and L.
+// Pass 2: the log-sum-exp merge.  Its arithmetic, per output dim d:
+//   M     = max of the live splits' m_s;  w_s = e^{m_s - M}
+//   a_j   = fma chain over s = j, j + 64, j + 128, ... < live of (o_s[d], w_s),
+//   l_j   = the same chain of (l_s, w_s), both from 0, for split lanes j < 64
+//   total = ((0 + a_0) + a_1) + ... + a_63,  L likewise;  out[d] = total / L
+// (lanes without a live split add +0).  Two layouts compute exactly this:
+//
+// Units (q head, head / 32 dim slices) of a workgroup: lane (split lane sl,
+// dim quarter) covers splits sl, sl + 64, ...; with up to COMB_ROUNDS * 64
+// live splits it loads each split's max, sum and 8 of the slice's dims in
+// one round trip and keeps them in registers while the workgroup max M
+// forms (more splits take a second pass over the buffer); the split lanes
+// are summed through LDS.  Every workgroup of a head computes the same M.
+// Used where the split count is large (decode at long context).
+//
+// attention_combine_wave: one wave per q head, lane l owning dims 2l and
+// 2l + 1, walking the split lanes in order.  Used for many query tokens with
+// few live splits each (prefill), where a workgroup per 32 dims would be
+// mostly idle lanes.
 #define COMB_SPLIT_LANES 64
 #define COMB_ROUNDS 4
 // LDS floats of one combine unit: per split lane 32 dims + 1 pad, its sum,
@@ -585,9 +596,9 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     for (int r = 0; r < COMB_ROUNDS; ++r) {
       if (sl + r * COMB_SPLIT_LANES >= live) break;
       const float w = expf(mv[r] - M);
-      if ((threadIdx.x & 3) == 0) l += lv[r] * w;
+      if ((threadIdx.x & 3) == 0) l = fmaf(lv[r], w, l);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a[k] += dv[r][k] * w;
+      for (int k = 0; k < 8; ++k) a[k] = fmaf(dv[r][k], w, a[k]);
     }
   } else {
     float m = -INFINITY;
@@ -596,11 +607,11 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
       const float *row = base + (size_t)s * slot;
       const float w = expf(row[head] - M);
-      if ((threadIdx.x & 3) == 0) l += row[head + 1] * w;
+      if ((threadIdx.x & 3) == 0) l = fmaf(row[head + 1], w, l);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t d = d0 + dq + k;
-        if (d < head) a[k] += row[d] * w;
+        if (d < head) a[k] = fmaf(row[d], w, a[k]);
       }
     }
   }
@@ -616,5 +627,52 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     }
     const uint32_t d = d0 + threadIdx.x;
     if (d < head) st_out(out + d, total / L);
+  }
+}
+
+// The merge above for q head h by one wave (call with the whole wave).
+AMMON_DEV void attention_combine_wave(const ammon_k_attention &p, uint32_t h) {
+#pragma clang fp contract(off)
+  const uint32_t lane = threadIdx.x & 63;
+  const uint32_t head = p.head, slot = head + 2;
+  const bool mine = 2 * lane < head;
+  float *out = p.out + (size_t)h * head + 2 * lane;
+  const uint32_t pos = p.step->position + p.pos_add;
+  if (pos >= p.seq) {
+    if (mine) {
+      st_out(out, __uint_as_float(0x7fc00000u));
+      st_out(out + 1, __uint_as_float(0x7fc00000u));
+    }
+    return;
+  }
+  const uint32_t live = min(pos / p.split_len + 1, p.splits);
+  const float *base = p.partial + (size_t)h * p.splits * slot;
+  float m = -INFINITY;
+  for (uint32_t s = lane; s < live; s += COMB_SPLIT_LANES) m = fmaxf(m, base[(size_t)s * slot + head]);
+  const float M = wave_max(m);
+  const uint32_t d = mine ? 2 * lane : 0;
+  float t0 = 0.f, t1 = 0.f, L = 0.f;
+  const uint32_t lanes = min(live, (uint32_t)COMB_SPLIT_LANES);
+  for (uint32_t j = 0; j < lanes; ++j) {
+    float a0 = 0.f, a1 = 0.f, l = 0.f;
+    for (uint32_t s = j; s < live; s += COMB_SPLIT_LANES) {
+      const float *row = base + (size_t)s * slot;
+      const float w = expf(row[head] - M);
+      l = fmaf(row[head + 1], w, l);
+      a0 = fmaf(row[d], w, a0);
+      a1 = fmaf(row[d + 1], w, a1);
+    }
+    t0 = t0 + a0;
+    t1 = t1 + a1;
+    L = L + l;
+  }
+  if (lanes < COMB_SPLIT_LANES) {  // the idle split lanes' +0
+    t0 = t0 + 0.f;
+    t1 = t1 + 0.f;
+    L = L + 0.f;
+  }
+  if (mine) {
+    st_out(out, t0 / L);
+    st_out(out + 1, t1 / L);
   }
 }

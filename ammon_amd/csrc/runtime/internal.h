@@ -31,6 +31,7 @@ struct Kernels {
   // head-128 specialisations: [dtype][group index], widest chunk only
   hipFunction_t att_partial_h128[2][kAttGroups] = {};
   hipFunction_t att_combine = nullptr;
+  hipFunction_t att_combine_waves = nullptr;  // one wave per (token, q head)
   hipFunction_t gemv[2][2][kGemvModes] = {};
   hipFunction_t gemv_argmax[2][2] = {};  // PLAIN_ARGMAX: [dtype][vector?]
   hipFunction_t swiglu = nullptr;
@@ -54,6 +55,7 @@ constexpr uint32_t kGemvRowsPerWave = 2;
 constexpr uint32_t kGemvTileChunks = 4;  // U: chunks per lane per tile
 constexpr uint32_t kGemvWaves = 4;
 constexpr uint32_t kWorkgroup = 256;
+constexpr uint32_t kWaves = kWorkgroup / 64;
 
 // Resident workgroups of `f` per CU at 256 threads and `shmem` bytes of
 // dynamic LDS (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor, cached).

@@ -428,7 +428,7 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
                          q_heads, kv_heads, head, seq, split_len, splits, 0};
   st = launch3(rt, stream, f, splits, kv_heads, tokens, 0, p, "attention_prefill");
   if (st != AMMON_OK) return st;
-  return launch3(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), tokens, 0, p,
+  return launch3(rt, stream, rt->k.att_combine_waves, cdiv(q_heads, kWaves), 1, tokens, 0, p,
                  "attention_prefill");
 }
 

@@ -98,6 +98,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   R(2, "ammon_rope", k.rope);
   R(2, "ammon_cache_store", k.cache_store);
   R(3, "ammon_attention_combine", k.att_combine);
+  R(3, "ammon_attention_combine_waves", k.att_combine_waves);
   const char *dtn[2] = {"f32", "bf16"};
   const int chs[kAttChunks] = {8, 4, 2, 1};
   const int gs[kAttGroups] = {1, 2, 4, 8};

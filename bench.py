@@ -367,7 +367,11 @@ def main():
         rt.fill_normal(k, BF16, kv_n, 7, 2 * l)
         rt.fill_normal(v, BF16, kv_n, 7, 2 * l + 1)
     rt.synchronize()
-    log(f"weights + KV prefill in {time.time() - t0:.1f}s; launches/token={model.launches + 2}")
+    # the decode graph: the step's launch list with the LM head carrying the
+    # argmax's first pass, plus the argmax's second pass (one launch when
+    # persistent)
+    launches = 1 if args.persistent else model.launches + 1
+    log(f"weights + KV prefill in {time.time() - t0:.1f}s; launches/token={launches}")
 
     if args.copy_probe:
         copy_probe(rt)
@@ -432,7 +436,7 @@ def main():
             "batch": 1,
             "positions": [start_pos + args.warmup, c.max_seq - 1],
             "graph_replay": not args.no_graph,
-            "launches_per_token": model.launches + 2,
+            "launches_per_token": launches,
             "token_bytes": tok_bytes,
             "token_hbm_gbs": round(tok_bytes / (ms_per_step * 1e-3) / 1e9, 1),
             "token_roofline_frac": round(tok_bytes / (ms_per_step * 1e-3) / 1e9 / HBM_PEAK_GBS,

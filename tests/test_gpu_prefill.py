@@ -185,6 +185,8 @@ def test_prefill_qkv_positions_past_cache_poison_q(rt):
     (6, 6, 48, 256, 0, 9, 16, F32),
     (4, 2, 64, 80, 10, 70, 8, F32),
     (8, 1, 128, 300, 250, 50, 32, F32),
+    (4, 2, 64, 1200, 1100, 5, 8, F32),    # 138..139 live splits: several per split lane
+    (2, 1, 32, 4200, 4100, 3, 8, BF16),   # 513+: the decode merge's second pass
 ])
 def test_attention_prefill_equals_decode_per_token(rt, q_heads, kv_heads, head, seq, p0, T, split,
                                                   kv_dtype):
