@@ -376,6 +376,281 @@ AMMON_DEV void gemm(const ammon_k_gemm &p) {
   tile.epilogue(acc, xs);
 }
 
+// ---- long prompts: register-blocked tiles ----------------------------------
+// For prompts of 64 tokens and more a workgroup owns 64 tokens (4 column
+// tiles) x 4 waves x RT 16-row tiles per wave.  Every B fragment (x part)
+// read from LDS feeds RT MFMAs and every A fragment (W) 12, so a wave issues
+// 3 NT RT MFMAs per 32-wide step against 3 NT LDS and RT global 16-byte
+// reads per lane (the 16-row tiles above: 6 MFMAs per 6 LDS reads), and the
+// x chunk is staged once for 64 RT rows.  W streams six steps (three chunks)
+// ahead of use in registers and x two chunks ahead, so a workgroup's chain
+// of chunks is not paced by memory latency; x is staged in three LDS
+// buffers, one barrier per chunk.  The
+// arithmetic per output is the 16-row tiles' (W x hi, W x mid, W x lo per
+// step, fp32 accumulation) in the same order.  SWIGLU: a wave's first RT/2
+// tiles are gate rows, the last RT/2 the same up rows, paired in registers.
+template <int MODE, uint32_t RT, uint32_t NT_>
+struct BigTile {
+  static constexpr uint32_t NT = NT_, TB = 16 * NT, KC = 64, S = KC / 32;
+  static constexpr uint32_t RW = 16 * RT;                // virtual rows per wave
+  static constexpr uint32_t RBW = RW * AMMON_WAVES;      // virtual rows per workgroup
+  static constexpr uint32_t KG = KC / 8;
+  static constexpr uint32_t XU = TB * KG / AMMON_WG;     // x units per thread per chunk
+  static constexpr uint32_t QUADS = S * NT * 3 * 64;     // LDS quads per x buffer
+  static_assert(RT == 1 || RT % 2 == 0, "gate/up tile pairs");
+
+  ammon_k_gemm p;  // by value (see GemmTile)
+  uint32_t lane, tok0, row_bytes;
+  uint32_t vr[RT];  // first virtual row (SWIGLU: hidden row) of each tile
+  __amdgpu_buffer_rsrc_t r[RT];
+
+  AMMON_DEV BigTile(const ammon_k_gemm &p_, uint32_t rb, uint32_t tt) : p(p_) {
+    lane = threadIdx.x & 63;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    tok0 = tt * TB;
+    row_bytes = p.n * 2;
+    auto rsrc = [&](const void *base, uint32_t first, uint32_t limit) {
+      const uint32_t valid = first < limit ? min(16u, limit - first) : 0;
+      return make_rsrc((const uint16_t *)base + (size_t)(valid ? first : 0) * p.n,
+                       valid * row_bytes);
+    };
+#pragma unroll
+    for (uint32_t j = 0; j < RT; ++j) {
+      if (MODE == AMMON_GEMV_SWIGLU) {
+        const uint32_t h = rb * (RBW / 2) + wave * (RW / 2) + 16 * (j % (RT / 2));
+        vr[j] = h;
+        r[j] = rsrc(j < RT / 2 ? p.w0 : p.w1, h, p.d);
+      } else {
+        const uint32_t v = rb * RBW + wave * RW + 16 * j;
+        vr[j] = v;
+        if (MODE == AMMON_GEMV_QKV) {
+          const uint32_t kvd = p.kv_dim;
+          if (v < p.d)
+            r[j] = rsrc(p.w0, v, p.d);
+          else if (v < p.d + kvd)
+            r[j] = rsrc(p.w1, v - p.d, kvd);
+          else
+            r[j] = rsrc(p.w2, v - p.d - kvd, kvd);
+        } else {
+          r[j] = rsrc(p.w0, v, p.rows);
+        }
+      }
+    }
+  }
+
+  // W of 32-wide step g (k past the row end reads zero).
+  AMMON_DEV void load_w(uint32_t g, u32x4 (&a)[RT]) const {
+    const uint32_t k = 32 * g + 8 * (lane >> 4);
+    const uint32_t off = k < p.n ? (lane & 15) * row_bytes + k * 2 : AMMON_OOB;
+#pragma unroll
+    for (uint32_t j = 0; j < RT; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r[j], off, 0, 0);
+  }
+
+  // x unit u (8 consecutive k of one token) of a chunk: the 64 units of
+  // each group u / 64 are one (step, column tile) B fragment in lane order,
+  // so a wave stages a contiguous 1 KiB of LDS per part (no bank conflicts).
+  AMMON_DEV static void unit(uint32_t u, uint32_t &s, uint32_t &c, uint32_t &l, uint32_t &t,
+                             uint32_t &kg) {
+    const uint32_t g = u >> 6;
+    l = u & 63;
+    c = g % NT;
+    s = g / NT;
+    t = 16 * c + (l & 15);
+    kg = 4 * s + (l >> 4);
+  }
+
+  AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[XU][2]) const {
+    const __amdgpu_buffer_rsrc_t xr =
+        make_rsrc(p.x + (size_t)tok0 * p.n, (min(p.tokens - tok0, TB)) * p.n * 4);
+#pragma unroll
+    for (uint32_t m = 0; m < XU; ++m) {
+      uint32_t s, c, l, t, kg;
+      unit(threadIdx.x + AMMON_WG * m, s, c, l, t, kg);
+      const uint32_t k = ch * KC + 8 * kg;
+      const uint32_t off = k < p.n ? (t * p.n + k) * 4 : AMMON_OOB;
+      x[m][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
+      x[m][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
+    }
+  }
+
+  AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
+    return ((s * NT + c) * 3 + q) * 64 + l;
+  }
+
+  AMMON_DEV void stage(const u32x4 (&x)[XU][2], u32x4 *xs) const {
+#pragma unroll
+    for (uint32_t m = 0; m < XU; ++m) {
+      uint32_t s, c, l, t, kg;
+      unit(threadIdx.x + AMMON_WG * m, s, c, l, t, kg);
+      const f32x4 a = __builtin_bit_cast(f32x4, x[m][0]), b = __builtin_bit_cast(f32x4, x[m][1]);
+      const f32x8 f = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+      const bf16x8 hi = __builtin_convertvector(f, bf16x8);
+      const f32x8 r1 = f - __builtin_convertvector(hi, f32x8);
+      const bf16x8 mid = __builtin_convertvector(r1, bf16x8);
+      const f32x8 r2 = r1 - __builtin_convertvector(mid, f32x8);
+      const bf16x8 lo = __builtin_convertvector(r2, bf16x8);
+      xs[quad(s, c, 0, l)] = __builtin_bit_cast(u32x4, hi);
+      xs[quad(s, c, 1, l)] = __builtin_bit_cast(u32x4, mid);
+      xs[quad(s, c, 2, l)] = __builtin_bit_cast(u32x4, lo);
+    }
+  }
+
+  // Step s of the staged chunk: per column tile the three x parts, each
+  // against every row tile.  Straight-line code: a column tile past the
+  // last token multiplies staged zeros rather than branching, so the LDS
+  // reads of the whole step can be issued ahead of the MFMAs.
+  AMMON_DEV void compute(uint32_t s, const u32x4 *xs, const u32x4 (&a)[RT],
+                         f32x4 (&acc)[RT][NT]) const {
+#pragma unroll
+    for (uint32_t c = 0; c < NT; ++c) {
+#pragma unroll
+      for (int q = 0; q < 3; ++q) {
+        const bf16x8 b = __builtin_bit_cast(bf16x8, xs[quad(s, c, q, lane)]);
+#pragma unroll
+        for (uint32_t j = 0; j < RT; ++j)
+          acc[j][c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+              __builtin_bit_cast(bf16x8, a[j]), b, acc[j][c], 0, 0, 0);
+      }
+    }
+  }
+
+  // Lane l holds rows 4(l / 16)..+3 of each tile for token tok0 + 16c + l % 16.
+  AMMON_DEV void epilogue(const f32x4 (&acc)[RT][NT]) const {
+    const uint32_t rq = 4 * (lane >> 4);
+#pragma unroll
+    for (uint32_t c = 0; c < NT; ++c) {
+      const uint32_t t = tok0 + 16 * c + (lane & 15);
+      if (t >= p.tokens) continue;
+      if (MODE == AMMON_GEMV_SWIGLU) {
+#pragma unroll
+        for (uint32_t j = 0; j < RT / 2; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t h = vr[j] + rq + i;
+            if (h >= p.d) continue;
+            const float gate = acc[j][c][i], up = acc[j + RT / 2][c][i];
+            float v = gate * (1.0f / (1.0f + expf(-gate)));
+            v = v * up;
+            p.y[(size_t)t * p.d + h] = v;
+          }
+      } else if (MODE == AMMON_GEMV_QKV) {
+#pragma clang fp contract(off)
+        const uint32_t pos = p.step->position + t;
+        const uint32_t kvd = p.kv_dim;
+#pragma unroll
+        for (uint32_t j = 0; j < RT; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; i += 2) {
+            const uint32_t v = vr[j] + rq + i;
+            if (v >= p.rows) continue;
+            const float a0 = acc[j][c][i], a1 = acc[j][c][i + 1];
+            if (pos >= p.seq) {  // out-of-range position: poison q, touch no cache
+              if (v < p.d) {
+                p.y[(size_t)t * p.d + v] = __uint_as_float(0x7fc00000u);
+                p.y[(size_t)t * p.d + v + 1] = __uint_as_float(0x7fc00000u);
+              }
+              continue;
+            }
+            if (v < p.d + kvd) {
+              const uint32_t rr = v < p.d ? v : v - p.d;
+              const uint32_t hd = rr % p.head;
+              const float *cs = p.table + ((size_t)pos * (p.head / 2) + hd / 2) * 2;
+              const float fcr = cs[0], fci = cs[1];
+              const float o0 = a0 * fcr - a1 * fci;
+              const float o1 = a0 * fci + a1 * fcr;
+              if (v < p.d) {
+                p.y[(size_t)t * p.d + v] = o0;
+                p.y[(size_t)t * p.d + v + 1] = o1;
+              } else {
+                store_pair_out(p.k_cache, p.kv_dtype,
+                               ((size_t)(rr / p.head) * p.seq + pos) * p.head + hd, o0, o1);
+              }
+            } else {
+              const uint32_t rv = v - p.d - kvd;
+              store_pair_out(p.v_cache, p.kv_dtype,
+                             ((size_t)(rv / p.head) * p.seq + pos) * p.head + rv % p.head, a0, a1);
+            }
+          }
+      } else {
+#pragma unroll
+        for (uint32_t j = 0; j < RT; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t v = vr[j] + rq + i;
+            if (v >= p.rows) continue;
+            const size_t at = (size_t)t * p.d + v;
+            p.y[at] = MODE == AMMON_GEMV_RESIDUAL ? p.residual[at] + acc[j][c][i] : acc[j][c][i];
+          }
+      }
+    }
+  }
+};
+
+template <int MODE, uint32_t RT, uint32_t NT>
+AMMON_DEV void gemm_big(const ammon_k_gemm &p) {
+  using T = BigTile<MODE, RT, NT>;
+  __shared__ u32x4 xs[3][T::QUADS];
+  const uint32_t tiles = (p.tokens + T::TB - 1) / T::TB;
+  const uint32_t q = blockIdx.x >> 3;
+  const uint32_t rb = (q / tiles) * 8 + (blockIdx.x & 7u), tt = q % tiles;
+  const uint32_t covered = MODE == AMMON_GEMV_SWIGLU ? p.d : p.rows;
+  const uint32_t per = MODE == AMMON_GEMV_SWIGLU ? T::RBW / 2 : T::RBW;
+  if (rb * per >= covered) return;  // padding of the last group (uniform)
+  T tile(p, rb, tt);
+  f32x4 acc[RT][T::NT];
+#pragma unroll
+  for (uint32_t j = 0; j < RT; ++j)
+#pragma unroll
+    for (uint32_t c = 0; c < T::NT; ++c) acc[j][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+  const uint32_t chunks = (p.n + T::KC - 1) / T::KC;
+  // rings: W of steps 2ch .. 2ch + 5 (a0..a5), x of chunks ch .. ch + 2
+  // (x0..x2), LDS buffer ch % 3
+  u32x4 a0[RT], a1[RT], a2[RT], a3[RT], a4[RT], a5[RT];
+  u32x4 x0[T::XU][2], x1[T::XU][2], x2[T::XU][2];
+  tile.load_w(0, a0);
+  tile.load_w(1, a1);
+  tile.load_x(0, x0);
+  tile.load_w(2, a2);
+  tile.load_w(3, a3);
+  tile.load_x(1, x1);
+  tile.load_w(4, a4);
+  tile.load_w(5, a5);
+  // Chunk c: stage its x (loaded two chunks ago) into LDS buffer c % 3,
+  // then request x of chunk c + 2 and, as each step's W is used, the W six
+  // steps on.  Buffer c % 3 was last read for chunk c - 3, which every wave
+  // finished before the barrier of chunk c - 2.  Requests past the end read
+  // zero without touching memory; they are issued anyway so that every path
+  // into the loop has the same loads in flight in the same order (the
+  // compiler's wait counts then leave the prefetches outstanding).
+  // The scheduling barriers pin the issue order of the phases: the memory
+  // counters complete in order, so a load moved later would make every
+  // older prefetch wait for it.
+#define BIG_CHUNK(C, XS, XC, XN, WA, WB)                 \
+  {                                                      \
+    tile.stage(XC, xs[XS]);                              \
+    __syncthreads();                                     \
+    tile.load_x((C) + 2, XN);                            \
+    __builtin_amdgcn_sched_barrier(0);                   \
+    tile.compute(0, xs[XS], WA, acc);                    \
+    __builtin_amdgcn_sched_barrier(0);                   \
+    tile.load_w(2 * (C) + 6, WA);                        \
+    __builtin_amdgcn_sched_barrier(0);                   \
+    tile.compute(1, xs[XS], WB, acc);                    \
+    __builtin_amdgcn_sched_barrier(0);                   \
+    tile.load_w(2 * (C) + 7, WB);                        \
+    __builtin_amdgcn_sched_barrier(0);                   \
+  }
+  // Whole rounds of three chunks: one or two chunks past the end multiply
+  // zeros (adding nothing), which keeps the loop body free of exits.
+  for (uint32_t ch = 0; ch < chunks; ch += 3) {
+    BIG_CHUNK(ch, 0, x0, x2, a0, a1)
+    BIG_CHUNK(ch + 1, 1, x1, x0, a2, a3)
+    BIG_CHUNK(ch + 2, 2, x2, x1, a4, a5)
+  }
+#undef BIG_CHUNK
+  tile.epilogue(acc);
+}
+
 }  // namespace
 
 #define GEMM_KERNEL(NAME, WT, MODE, NT, KC, KS)                                    \
@@ -397,3 +672,18 @@ AMMON_DEV void gemm(const ammon_k_gemm &p) {
 
 GEMM_MODES(bf16, uint16_t, 512)
 GEMM_MODES(f32, float, 256)
+
+// long prompts, bf16 W: 16 NT-token tiles, RT 16-row tiles per wave
+#define GEMM_BIG_KERNEL(NAME, MODE, RT, NT)                                        \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemm p) { \
+    gemm_big<MODE, RT, NT>(p);                                                   \
+  }
+#define GEMM_BIG_MODES(SUFFIX, RT, NT)                                                 \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_plain_##SUFFIX, AMMON_GEMV_PLAIN, RT, NT)            \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_residual_##SUFFIX, AMMON_GEMV_RESIDUAL, RT, NT)      \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_swiglu_##SUFFIX, AMMON_GEMV_SWIGLU, RT, NT)          \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_qkv_##SUFFIX, AMMON_GEMV_QKV, RT, NT)
+GEMM_BIG_MODES(t64_r4, 4, 4)
+GEMM_BIG_MODES(t64_r2, 2, 4)
+GEMM_BIG_MODES(t32_r4, 4, 2)
+GEMM_BIG_MODES(t32_r2, 2, 2)

@@ -45,6 +45,8 @@ struct Kernels {
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]
   // [row tile per wave / split over the workgroup's waves][mode]
   hipFunction_t gemm[2][2][2][kGemvModes] = {};
+  // bf16, register-blocked tiles: [64 tokens, 32 tokens][RT 4, RT 2][mode]
+  hipFunction_t gemm_big[2][2][kGemvModes] = {};
 };
 
 // LDS per compute unit on gfx950 (bytes); bounds resident GEMV workgroups.
@@ -93,6 +95,10 @@ struct ammon_runtime {
   ammon_device_info info = {};
   uint32_t gemv_wgs_per_cu = 4;
   int gemm_split = -1;  // prefill GEMM reduction split: -1 by shape, 0 never, 1 always
+  // prefill GEMM register-blocked tiles (bf16, >= 64 tokens): -1 by shape,
+  // 0 never, else 10 * tokens-per-tile / 16 + 16-row tiles per wave
+  // (44, 42, 24, 22)
+  int gemm_big = -1;
   std::mutex occ_mu;
   std::map<std::pair<hipFunction_t, size_t>, uint32_t> occ_cache;
 };

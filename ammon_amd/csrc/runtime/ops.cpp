@@ -486,6 +486,41 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   p.head = a.head;
   p.seq = a.seq;
   p.kv_dtype = (uint32_t)a.kv_dtype;
+  // bf16 W: register-blocked tiles of 64 or 32 tokens x 4 waves x 4 or 2
+  // 16-row tiles per wave.  The largest tile whose grid still gives at least
+  // 3/4 of a workgroup per CU, else (64+ tokens) the smallest; below 64
+  // tokens a projection that cannot fill the device that way keeps the
+  // 16/32-token tiles below, whose reduction split over the waves suits few
+  // rows.  Measured on the Llama-3-8B projections at 16..512 tokens.
+  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
+  if (a.w_dtype == AMMON_BF16 && rt->gemm_big != 0) {
+    const uint32_t covered = a.mode == AMMON_GEMV_SWIGLU ? a.d : a.rows;
+    const uint32_t per4 = a.mode == AMMON_GEMV_SWIGLU ? 128 : 256;  // RT 4: rows per workgroup
+    auto wgs = [&](int t64, int rt4) {
+      return (uint64_t)cdiv(covered, rt4 ? per4 : per4 / 2) * cdiv(a.tokens, t64 ? 64 : 32);
+    };
+    int t64 = -1, rt4 = 0;
+    if (rt->gemm_big > 0) {
+      t64 = rt->gemm_big / 10 == 4;
+      rt4 = rt->gemm_big % 10 == 4;
+    } else {
+      const int order[4][2] = {{1, 1}, {1, 0}, {0, 1}, {0, 0}};
+      for (const auto &o : order)
+        if ((a.tokens >= 64 || !o[0]) && wgs(o[0], o[1]) * 4 >= (uint64_t)cus * 3) {
+          t64 = o[0];
+          rt4 = o[1];
+          break;
+        }
+      if (t64 < 0 && a.tokens >= 64) t64 = rt4 = 0;
+    }
+    if (t64 >= 0) {
+      const uint64_t tiles = cdiv(a.tokens, t64 ? 64 : 32);
+      const uint64_t groups = cdiv(cdiv(covered, rt4 ? per4 : per4 / 2), 8);
+      AMMON_CHECK(groups * 8 * tiles < (1ull << 31), "%s: grid too large", what);
+      return launch(rt, stream, rt->k.gemm_big[t64 ? 0 : 1][rt4 ? 0 : 1][a.mode],
+                    (uint32_t)(groups * 8 * tiles), 1, 0, p, what);
+    }
+  }
   // 64 virtual rows x 16 tokens per workgroup for short prompts, x 32 beyond;
   // 16 rows (the reduction split over the four waves) when 64-row tiles
   // would occupy at most a quarter of the CUs -- measured at the
@@ -495,7 +530,6 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   // kernel maps a 1-D grid of (row-block groups of 8) x token tiles x 8.
   const int wide = a.tokens > 16 ? 1 : 0;
   const uint64_t tiles = cdiv(a.tokens, wide ? 32 : 16);
-  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
   const int split = rt->gemm_split >= 0 ? rt->gemm_split
                                         : ((uint64_t)cdiv(a.rows, 64) * tiles * 4 <= cus ? 1 : 0);
   hipFunction_t f = rt->k.gemm[a.w_dtype == AMMON_BF16 ? 1 : 0][wide][split][a.mode];

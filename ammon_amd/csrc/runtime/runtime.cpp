@@ -153,6 +153,14 @@ static ammon_status load_kernels(ammon_runtime *rt) {
                    s ? "_k4" : "");
           R(7, name, k.gemm[d][t][s][m]);
         }
+  for (int t = 0; t < 2; ++t)
+    for (int r = 0; r < 2; ++r)
+      for (int m = 0; m < kGemvModes; ++m) {
+        char name[96];
+        snprintf(name, sizeof name, "ammon_gemm_bf16_%s_t%d_r%d", modes[m], t ? 32 : 64,
+                 r ? 2 : 4);
+        R(7, name, k.gemm_big[t][r][m]);
+      }
 #undef R
   return AMMON_OK;
 }
@@ -197,6 +205,10 @@ static ammon_status create(int device, ammon_runtime **out) {
   if (const char *env = std::getenv("AMMON_GEMM_SPLIT")) {
     const int v = std::atoi(env);
     if (v == 0 || v == 1) rt->gemm_split = v;
+  }
+  if (const char *env = std::getenv("AMMON_GEMM_BIG")) {
+    const int v = std::atoi(env);
+    if (v == 0 || v == 44 || v == 42 || v == 24 || v == 22) rt->gemm_big = v;
   }
   if (const char *env = std::getenv("AMMON_GEMV_WGS_PER_CU")) {
     int v = std::atoi(env);

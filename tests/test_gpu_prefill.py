@@ -54,10 +54,13 @@ def pos_major(hm, kv_heads, seq, head):
 # a 256-wide chunk (288 = 256 + 32), tokens past 16- and 32-token tiles.  The
 # library splits the reduction over a workgroup's waves (16-row tiles) when
 # 64-row tiles would not fill the device; the last two shapes take 64-row
-# tiles (16- and 32-token variants).
+# tiles (16- and 32-token variants).  From 64 tokens bf16 weights take 64-token
+# tiles with 2 or 4 16-row tiles per wave: tails in rows (520, 1000), in the
+# 64-wide reduction chunks (4104, 520) and in tokens (130 = 2 * 64 + 2).
 GEMM_SHAPES = [(4096, 4096, 16), (1024, 4096, 33), (288, 288, 8), (768, 288, 40),
                (288, 768, 7), (100, 264, 5), (5, 8, 3), (64, 256, 1), (130, 4104, 64),
-               (32768, 64, 16), (4096, 264, 256)]
+               (32768, 64, 16), (4096, 264, 256), (1000, 520, 130), (520, 4104, 64),
+               (8192, 1024, 100)]
 
 
 @pytest.mark.parametrize("d,n,tokens", GEMM_SHAPES)
@@ -103,7 +106,8 @@ def test_prefill_gemm_validation(rt):
 
 @pytest.mark.parametrize("dim,hidden,tokens,w_dtype",
                          [(288, 768, 8, F32), (4096, 14336, 16, BF16), (64, 200, 35, BF16),
-                          (64, 16400, 16, BF16), (64, 4100, 100, F32)])
+                          (64, 16400, 16, BF16), (64, 4100, 100, F32), (256, 1000, 130, BF16),
+                          (512, 8192, 64, BF16)])
 def test_prefill_gate_up_swiglu(rt, dim, hidden, tokens, w_dtype):
     w1 = oracle.storage(oracle.normal(hidden * dim, 211, std=0.02), w_dtype).reshape(hidden, dim)
     w3 = oracle.storage(oracle.normal(hidden * dim, 212, std=0.02), w_dtype).reshape(hidden, dim)
@@ -244,7 +248,8 @@ def test_model_prefill_matches_stepping(rt, heads, kv_dtype, w_dtype):
                              max_seq=300, theta=500000.0, w_dtype=w_dtype, kv_dtype=kv_dtype)
     stepped = LlamaModel.synthetic(rt, cfg, seed=41, std=0.05)
     filled = LlamaModel(rt, cfg, stepped.weights)
-    prompt = [int(t) for t in np.arange(37) * 131 % 5003]
+    # 100 tokens: the 64-token GEMM tiles for bf16 weights
+    prompt = [int(t) for t in np.arange(100) * 131 % 5003]
     for pos, tok in enumerate(prompt):
         want = stepped.step(tok, pos)
     got = filled.prefill(prompt)
