@@ -140,14 +140,27 @@ struct GemmTile {
     }
   }
 
-  // x of chunk `ch`: unit u = tid + 256 m is (token u / KG, 8-wide k group
-  // u % KG); tokens and k past the end read as zero (no branches).
+  // x unit u = tid + 256 m of chunk `ch` (8 consecutive k of one token):
+  // the 64 units of each group u / 64 are one (step, column tile) B fragment
+  // in lane order, so a wave stages a contiguous 1 KiB of LDS per part (no
+  // bank conflicts); tokens and k past the end read as zero (no branches).
+  AMMON_DEV static void unit(uint32_t u, uint32_t &s, uint32_t &c, uint32_t &l, uint32_t &t,
+                             uint32_t &kg) {
+    const uint32_t g = u >> 6;
+    l = u & 63;
+    c = g % NT;
+    s = g / NT;
+    t = 16 * c + (l & 15);
+    kg = 4 * s + (l >> 4);
+  }
+
   AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[XU][2]) const {
     const __amdgpu_buffer_rsrc_t xr = make_rsrc(p.x + (size_t)tok0 * p.n, (min(p.tokens - tok0, TB)) * p.n * 4);
 #pragma unroll
     for (uint32_t m = 0; m < XU; ++m) {
-      const uint32_t u = threadIdx.x + AMMON_WG * m;
-      const uint32_t t = u / KG, k = ch * KC + 8 * (u % KG);
+      uint32_t s, c, l, t, kg;
+      unit(threadIdx.x + AMMON_WG * m, s, c, l, t, kg);
+      const uint32_t k = ch * KC + 8 * kg;
       const uint32_t off = k < p.n ? (t * p.n + k) * 4 : AMMON_OOB;
       x[m][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
       x[m][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
@@ -162,9 +175,8 @@ struct GemmTile {
   AMMON_DEV void stage(const u32x4 (&x)[XU][2], u32x4 *xs) const {
 #pragma unroll
     for (uint32_t m = 0; m < XU; ++m) {
-      const uint32_t u = threadIdx.x + AMMON_WG * m;
-      const uint32_t t = u / KG, kg = u % KG;
-      const uint32_t s = kg >> 2, c = t >> 4, l = (t & 15) + 16 * (kg & 3);
+      uint32_t s, c, l, t, kg;
+      unit(threadIdx.x + AMMON_WG * m, s, c, l, t, kg);
       if constexpr (sizeof(WT) == 2) {
         const f32x4 a = __builtin_bit_cast(f32x4, x[m][0]), b = __builtin_bit_cast(f32x4, x[m][1]);
         const f32x8 f = {a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
