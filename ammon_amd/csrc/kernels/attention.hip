@@ -34,8 +34,11 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
   ATT_PARTIAL(PREFIX##_g4, KV, CH, 4, 128, true)       \
   ATT_PARTIAL(PREFIX##_g8, KV, CH, 8, 128, true)
 
-// bf16 K/V: q.k on matrix cores, two chunk buffers (four measured no faster
-// here: one workgroup per unit already keeps a 128-position split in flight)
+// bf16 K/V: q.k on matrix cores with two chunk buffers, one for the 4:1
+// group (the Llama-3 shape): at split 128 every workgroup requesting both of
+// its chunks at once delays all first chunks -- one buffer measured 0.1-0.7
+// us faster per launch at positions 1023..8191 (four buffers no faster than
+// two)
 #define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p0) { \
     __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
@@ -45,7 +48,7 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
   }
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1, 2)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2, 2)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4, 2)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4, 1)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 2)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
