@@ -3,13 +3,29 @@
 // = one pass with the workgroups of the grid, x staged in dynamic LDS.
 #include "gemv_impl.h"
 
-#define GEMV_KERNEL(NAME, WT, CH, RPW, U, MODE)                                 \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemv p) { \
-    extern __shared__ float4 xs4[];                                            \
-    __shared__ float red[AMMON_WAVES];                                         \
-    GemvPass<WT, CH, RPW, U, MODE> pass;                                       \
-    pass.begin(p, blockIdx.x, gridDim.x);                                      \
-    pass.run(xs4, red);                                                        \
+// The fields the first weight requests depend on come first as scalar
+// arguments, which this code object asks to have preloaded into SGPRs at
+// wave launch (-amdgpu-kernarg-preload-count): the requests then go out
+// without waiting for a kernel-argument load.  The parameter struct follows
+// (its copies of these fields are ignored).
+#define GEMV_KERNEL(NAME, WT, CH, RPW, U, MODE)                                          \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(                          \
+      const void *w0, const void *w1, const void *w2, uint32_t n, uint32_t rows,        \
+      uint32_t row_blocks, uint32_t d, uint32_t kv_dim, uint32_t nwg, ammon_k_gemv p0) { \
+    extern __shared__ float4 xs4[];                                                     \
+    __shared__ float red[AMMON_WAVES];                                                  \
+    ammon_k_gemv p = p0;                                                                \
+    p.w0 = w0;                                                                          \
+    p.w1 = w1;                                                                          \
+    p.w2 = w2;                                                                          \
+    p.n = n;                                                                            \
+    p.rows = rows;                                                                      \
+    p.row_blocks = row_blocks;                                                          \
+    p.d = d;                                                                            \
+    p.kv_dim = kv_dim;                                                                  \
+    GemvPass<WT, CH, RPW, U, MODE> pass;                                                \
+    pass.begin(p, blockIdx.x, nwg);                                                     \
+    pass.run(xs4, red);                                                                 \
   }
 
 #define GEMV_MODES(PREFIX, WT, CH, RPW, U)                                    \

@@ -162,7 +162,16 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     AMMON_CHECK(grid <= a.cand_cap, "%s: scratch holds %u candidates, the launch needs %u", what,
                 a.cand_cap, grid);
   if (grid_out) *grid_out = grid;
-  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
+  // the GEMV kernels' leading scalar arguments (preloaded into SGPRs), then
+  // the parameter struct
+  DeviceGuard guard(rt->device);
+  hipStream_t st = stream ? (hipStream_t)stream : rt->stream;
+  void *args[] = {&p.w0, &p.w1,   &p.w2,      &p.n,  &p.rows, &p.row_blocks,
+                  &p.d,  &p.kv_dim, &grid, &p};
+  hipError_t e = hipModuleLaunchKernel(fn, grid, 1, 1, kWorkgroup, 1, 1, (uint32_t)lds, st, args,
+                                       nullptr);
+  if (e != hipSuccess) return hip_error(e, what);
+  return AMMON_OK;
 }
 
 // ---- attention ------------------------------------------------------------------
