@@ -532,15 +532,16 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   }
   // 64 virtual rows x 16 tokens per workgroup for short prompts, x 32 beyond;
   // 16 rows (the reduction split over the four waves) when 64-row tiles
-  // would occupy at most a quarter of the CUs -- measured at the
-  // Llama-3-8B shape: the 4096-row projections run 1.6-1.9x faster split at
-  // up to 32 tokens, while 6144 rows break even and 28672 rows (gate/up)
-  // lose, every split x chunk being staged for a quarter of the rows.  The
-  // kernel maps a 1-D grid of (row-block groups of 8) x token tiles x 8.
+  // would occupy at most half of the CUs -- measured at the Llama-3-8B
+  // shape: the 4096-row projections run 1.2-1.9x faster split at up to 48
+  // tokens and the 6144-row QKV 1.1-1.5x up to 32 tokens, while QKV at 48
+  // tokens and the 28672 gate/up rows lose, every split x chunk being
+  // staged for a quarter of the rows.  The kernel maps a 1-D grid of
+  // (row-block groups of 8) x token tiles x 8.
   const int wide = a.tokens > 16 ? 1 : 0;
   const uint64_t tiles = cdiv(a.tokens, wide ? 32 : 16);
   const int split = rt->gemm_split >= 0 ? rt->gemm_split
-                                        : ((uint64_t)cdiv(a.rows, 64) * tiles * 4 <= cus ? 1 : 0);
+                                        : ((uint64_t)cdiv(a.rows, 64) * tiles * 4 <= 2 * cus ? 1 : 0);
   hipFunction_t f = rt->k.gemm[a.w_dtype == AMMON_BF16 ? 1 : 0][wide][split][a.mode];
   const uint64_t groups = cdiv(a.rows, (split ? 16 : 64) * 8);
   AMMON_CHECK(groups * 8 * tiles < (1ull << 31), "%s: grid too large", what);
