@@ -270,7 +270,7 @@ class LlamaModel : public AutoregressiveModel {
   std::vector<float> host_logits_;
   // prompt prefill scratch, [capacity, width] rows
   uint32_t pf_cap_ = 0;
-  Tensor pf_ids_, pf_x_, pf_xn_, pf_q_, pf_att_, pf_hb_, pf_partial_;
+  Tensor pf_ids_, pf_x_, pf_xn_, pf_q_, pf_att_, pf_hb_, pf_partial_, pf_ws_;
 };
 
 DType dt(ammon_dtype d) { return (DType)d; }
@@ -507,6 +507,10 @@ void LlamaModel::ensure_prefill(uint32_t n) {
   pf_q_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
   pf_att_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
   pf_hb_ = Tensor::zeros(rt_, Shape::from_dims({cap, c_.hidden}), DType::F32);
+  // split-reduction partial sums of the wo and w2 GEMMs ([tokens, dim] outputs)
+  pf_ws_ = Tensor::zeros(
+      rt_, Shape::vector((uint32_t)(ammon_prefill_gemm_workspace_bytes(c_.dim, cap) / 4)),
+      DType::F32);
   pf_cap_ = cap;
 }
 
@@ -562,14 +566,16 @@ void LlamaModel::prefill(const int32_t *tokens, uint32_t n, uint32_t start, floa
                                   c_.n_kv_heads, head_, c_.max_seq, step, ctx, split,
                                   (float *)pf_partial_.data(), part_bytes, att),
           "prefill attention");
-    check(ammon_prefill_gemm(rt, st, aw.output.data(), wd, c_.dim, q_dim_, att, n, x, x),
+    check(ammon_prefill_gemm_ws(rt, st, aw.output.data(), wd, c_.dim, q_dim_, att, n, x, x,
+                                pf_ws_.data(), pf_ws_.nbytes()),
           "prefill wo");
     check(ammon_rmsnorm(rt, st, x, fw.norm.data(), AMMON_F32, xn, n, c_.dim, c_.eps),
           "prefill rmsnorm");
     check(ammon_prefill_gate_up_swiglu(rt, st, xn, n, fw.gate.data(), fw.up.data(), wd, c_.dim,
                                        c_.hidden, hb),
           "prefill gate/up");
-    check(ammon_prefill_gemm(rt, st, fw.down.data(), wd, c_.dim, c_.hidden, hb, n, x, x),
+    check(ammon_prefill_gemm_ws(rt, st, fw.down.data(), wd, c_.dim, c_.hidden, hb, n, x, x,
+                                pf_ws_.data(), pf_ws_.nbytes()),
           "prefill w2");
   }
   check(ammon_gemv_rmsnorm(rt, st, x + (size_t)(n - 1) * c_.dim, rms_final_.data(), AMMON_F32,

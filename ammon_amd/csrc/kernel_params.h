@@ -125,6 +125,11 @@ typedef struct {
   const float *table;       /* QKV: rope cos/sin [seq, head/2, 2] */
   uint32_t d, n, rows, tokens;
   uint32_t kv_dim, head, seq, kv_dtype; /* QKV */
+  /* PLAIN / RESIDUAL, register-blocked tiles: the reduction split into
+   * ksplit ranges of kchunks 64-wide chunks; range s writes its partial
+   * sums to ws[s][tokens][d], summed in order by ammon_gemm_reduce */
+  float *ws;
+  uint32_t ksplit, kchunks;
 } ammon_k_gemm;
 
 typedef struct {

@@ -413,14 +413,17 @@ struct BigTile {
 
   ammon_k_gemm p;  // by value (see GemmTile)
   uint32_t lane, tok0, row_bytes;
+  uint32_t kbeg, kend;  // this workgroup's reduction range
   uint32_t vr[RT];  // first virtual row (SWIGLU: hidden row) of each tile
   __amdgpu_buffer_rsrc_t r[RT];
 
-  AMMON_DEV BigTile(const ammon_k_gemm &p_, uint32_t rb, uint32_t tt) : p(p_) {
+  AMMON_DEV BigTile(const ammon_k_gemm &p_, uint32_t rb, uint32_t tt, uint32_t ks) : p(p_) {
     lane = threadIdx.x & 63;
     const uint32_t wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     tok0 = tt * TB;
     row_bytes = p.n * 2;
+    kbeg = p.ksplit > 1 ? ks * p.kchunks * KC : 0;
+    kend = p.ksplit > 1 ? min(kbeg + p.kchunks * KC, p.n) : p.n;
     auto rsrc = [&](const void *base, uint32_t first, uint32_t limit) {
       const uint32_t valid = first < limit ? min(16u, limit - first) : 0;
       return make_rsrc((const uint16_t *)base + (size_t)(valid ? first : 0) * p.n,
@@ -450,10 +453,10 @@ struct BigTile {
     }
   }
 
-  // W of 32-wide step g (k past the row end reads zero).
+  // W of the range's 32-wide step g (k past the range reads zero).
   AMMON_DEV void load_w(uint32_t g, u32x4 (&a)[RT]) const {
-    const uint32_t k = 32 * g + 8 * (lane >> 4);
-    const uint32_t off = k < p.n ? (lane & 15) * row_bytes + k * 2 : AMMON_OOB;
+    const uint32_t k = kbeg + 32 * g + 8 * (lane >> 4);
+    const uint32_t off = k < kend ? (lane & 15) * row_bytes + k * 2 : AMMON_OOB;
 #pragma unroll
     for (uint32_t j = 0; j < RT; ++j) a[j] = __builtin_amdgcn_raw_buffer_load_b128(r[j], off, 0, 0);
   }
@@ -478,8 +481,8 @@ struct BigTile {
     for (uint32_t m = 0; m < XU; ++m) {
       uint32_t s, c, l, t, kg;
       unit(threadIdx.x + AMMON_WG * m, s, c, l, t, kg);
-      const uint32_t k = ch * KC + 8 * kg;
-      const uint32_t off = k < p.n ? (t * p.n + k) * 4 : AMMON_OOB;
+      const uint32_t k = kbeg + ch * KC + 8 * kg;
+      const uint32_t off = k < kend ? (t * p.n + k) * 4 : AMMON_OOB;
       x[m][0] = __builtin_amdgcn_raw_buffer_load_b128(xr, off, 0, 0);
       x[m][1] = __builtin_amdgcn_raw_buffer_load_b128(xr, off + 16, 0, 0);
     }
@@ -527,13 +530,22 @@ struct BigTile {
   }
 
   // Lane l holds rows 4(l / 16)..+3 of each tile for token tok0 + 16c + l % 16.
-  AMMON_DEV void epilogue(const f32x4 (&acc)[RT][NT]) const {
+  AMMON_DEV void epilogue(const f32x4 (&acc)[RT][NT], uint32_t ks) const {
     const uint32_t rq = 4 * (lane >> 4);
 #pragma unroll
     for (uint32_t c = 0; c < NT; ++c) {
       const uint32_t t = tok0 + 16 * c + (lane & 15);
       if (t >= p.tokens) continue;
-      if (MODE == AMMON_GEMV_SWIGLU) {
+      if ((MODE == AMMON_GEMV_PLAIN || MODE == AMMON_GEMV_RESIDUAL) && p.ksplit > 1) {
+        float *w = p.ws + ((size_t)ks * p.tokens + t) * p.d;  // this range's partial sums
+#pragma unroll
+        for (uint32_t j = 0; j < RT; ++j)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t v = vr[j] + rq + i;
+            if (v < p.rows) w[v] = acc[j][c][i];
+          }
+      } else if (MODE == AMMON_GEMV_SWIGLU) {
 #pragma unroll
         for (uint32_t j = 0; j < RT / 2; ++j)
 #pragma unroll
@@ -602,19 +614,23 @@ template <int MODE, uint32_t RT, uint32_t NT>
 AMMON_DEV void gemm_big(const ammon_k_gemm &p) {
   using T = BigTile<MODE, RT, NT>;
   __shared__ u32x4 xs[3][T::QUADS];
+  // id = ((row-block group, reduction range), token tile, XCD): the token
+  // tiles of a row block and range are adjacent on one XCD
   const uint32_t tiles = (p.tokens + T::TB - 1) / T::TB;
+  const uint32_t ksplit = p.ksplit > 1 ? p.ksplit : 1;
   const uint32_t q = blockIdx.x >> 3;
-  const uint32_t rb = (q / tiles) * 8 + (blockIdx.x & 7u), tt = q % tiles;
+  const uint32_t tt = q % tiles, ks = (q / tiles) % ksplit;
+  const uint32_t rb = (q / tiles / ksplit) * 8 + (blockIdx.x & 7u);
   const uint32_t covered = MODE == AMMON_GEMV_SWIGLU ? p.d : p.rows;
   const uint32_t per = MODE == AMMON_GEMV_SWIGLU ? T::RBW / 2 : T::RBW;
   if (rb * per >= covered) return;  // padding of the last group (uniform)
-  T tile(p, rb, tt);
+  T tile(p, rb, tt, ks);
   f32x4 acc[RT][T::NT];
 #pragma unroll
   for (uint32_t j = 0; j < RT; ++j)
 #pragma unroll
     for (uint32_t c = 0; c < T::NT; ++c) acc[j][c] = f32x4{0.f, 0.f, 0.f, 0.f};
-  const uint32_t chunks = (p.n + T::KC - 1) / T::KC;
+  const uint32_t chunks = (tile.kend - tile.kbeg + T::KC - 1) / T::KC;
   // rings: W of steps 2ch .. 2ch + 5 (a0..a5), x of chunks ch .. ch + 2
   // (x0..x2), LDS buffer ch % 3
   u32x4 a0[RT], a1[RT], a2[RT], a3[RT], a4[RT], a5[RT];
@@ -660,7 +676,7 @@ AMMON_DEV void gemm_big(const ammon_k_gemm &p) {
     BIG_CHUNK(ch + 2, 2, x2, x1, a4, a5)
   }
 #undef BIG_CHUNK
-  tile.epilogue(acc);
+  tile.epilogue(acc, ks);
 }
 
 }  // namespace
@@ -699,3 +715,15 @@ GEMM_BIG_MODES(t64_r4, 4, 4)
 GEMM_BIG_MODES(t64_r2, 2, 4)
 GEMM_BIG_MODES(t32_r4, 4, 2)
 GEMM_BIG_MODES(t32_r2, 2, 2)
+
+// y[t][r] = (residual[t][r] +) the split ranges' partial sums added in range
+// order: grid-stride over tokens x d.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_gemm_reduce(ammon_k_gemm p) {
+  const size_t total = (size_t)p.tokens * p.d;
+  for (size_t i = (size_t)blockIdx.x * AMMON_WG + threadIdx.x; i < total;
+       i += (size_t)gridDim.x * AMMON_WG) {
+    float acc = p.ws[i];
+    for (uint32_t s = 1; s < p.ksplit; ++s) acc = acc + p.ws[s * total + i];
+    p.y[i] = p.residual ? p.residual[i] + acc : acc;
+  }
+}

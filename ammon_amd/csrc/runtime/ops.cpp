@@ -457,6 +457,8 @@ struct GemmArgs {
   const float *table;
   uint32_t kv_dim, head, seq;
   ammon_dtype kv_dtype;
+  void *ws;  // PLAIN / RESIDUAL: optional workspace for a split reduction
+  size_t ws_bytes;
 };
 
 ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemmArgs &a,
@@ -475,6 +477,12 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   AMMON_CHECK(!overlaps(a.x, xbytes, a.y, a.y_bytes), "%s: y overlaps x", what);
   if (a.residual)
     AMMON_CHECK(!overlaps(a.x, xbytes, a.residual, a.y_bytes), "%s: residual overlaps x", what);
+  if (a.ws) {
+    AMMON_CHECK(!overlaps(a.ws, a.ws_bytes, a.x, xbytes) && !overlaps(a.ws, a.ws_bytes, a.y, a.y_bytes) &&
+                    !(a.residual && overlaps(a.ws, a.ws_bytes, a.residual, a.y_bytes)),
+                "%s: workspace overlaps x, y or residual", what);
+    AMMON_CHECK(((uintptr_t)a.ws & 15u) == 0, "%s: workspace must be 16-byte aligned", what);
+  }
   VALIDATE_ONLY();
   ammon_k_gemm p = {};
   p.w0 = a.w0;
@@ -496,11 +504,16 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   p.seq = a.seq;
   p.kv_dtype = (uint32_t)a.kv_dtype;
   // bf16 W: register-blocked tiles of 64 or 32 tokens x 4 waves x 4 or 2
-  // 16-row tiles per wave.  The largest tile whose grid still gives at least
-  // 3/4 of a workgroup per CU, else (64+ tokens) the smallest; below 64
-  // tokens a projection that cannot fill the device that way keeps the
-  // 16/32-token tiles below, whose reduction split over the waves suits few
-  // rows.  Measured on the Llama-3-8B projections at 16..512 tokens.
+  // 16-row tiles per wave, the reduction optionally split into 2..8 ranges
+  // (plain / residual with a workspace).  Take the largest tile whose grid,
+  // split into ranges of at least 16 chunks, gives at least 3/4 of a
+  // workgroup per CU, with the smallest split that does; else (64+ tokens,
+  // or a splittable reduction) the smallest tile split into ranges of at
+  // least 8 chunks; below 64 tokens a projection that fills the device no
+  // way keeps the 16/32-token tiles below, whose reduction split over the
+  // waves suits few rows.  Measured on the Llama-3-8B projections at
+  // 16..512 tokens (e.g. w2 at 512 tokens: 64-row x 64-token tiles split in
+  // two 197 us, unsplit 128-row x 64-token tiles 253 us).
   const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
   if (a.w_dtype == AMMON_BF16 && rt->gemm_big != 0) {
     const uint32_t covered = a.mode == AMMON_GEMV_SWIGLU ? a.d : a.rows;
@@ -508,6 +521,20 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     auto wgs = [&](int t64, int rt4) {
       return (uint64_t)cdiv(covered, rt4 ? per4 : per4 / 2) * cdiv(a.tokens, t64 ? 64 : 32);
     };
+    const uint32_t chunks = (uint32_t)cdiv(a.n, 64);
+    const bool splittable =
+        a.ws && (a.mode == AMMON_GEMV_PLAIN || a.mode == AMMON_GEMV_RESIDUAL);
+    // the most ranges of at least `len` chunks the workspace holds
+    auto kmax_of = [&](uint32_t len) {
+      uint32_t k = 1;
+      if (splittable)
+        while (k < 8 && chunks / (k * 2) >= len &&
+               (uint64_t)k * 2 * a.tokens * a.d * 4 <= a.ws_bytes)
+          k *= 2;
+      return k;
+    };
+    uint32_t kmax = kmax_of(16);
+    const uint64_t need = ((uint64_t)cus * 3 + 3) / 4;
     int t64 = -1, rt4 = 0;
     if (rt->gemm_big > 0) {
       t64 = rt->gemm_big / 10 == 4;
@@ -515,19 +542,33 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     } else {
       const int order[4][2] = {{1, 1}, {1, 0}, {0, 1}, {0, 0}};
       for (const auto &o : order)
-        if ((a.tokens >= 64 || !o[0]) && wgs(o[0], o[1]) * 4 >= (uint64_t)cus * 3) {
+        if ((a.tokens >= 64 || !o[0]) && wgs(o[0], o[1]) * kmax >= need) {
           t64 = o[0];
           rt4 = o[1];
           break;
         }
-      if (t64 < 0 && a.tokens >= 64) t64 = rt4 = 0;
+      if (t64 < 0 && (a.tokens >= 64 || splittable)) {
+        t64 = rt4 = 0;
+        kmax = kmax_of(8);
+      }
     }
     if (t64 >= 0) {
       const uint64_t tiles = cdiv(a.tokens, t64 ? 64 : 32);
       const uint64_t groups = cdiv(cdiv(covered, rt4 ? per4 : per4 / 2), 8);
-      AMMON_CHECK(groups * 8 * tiles < (1ull << 31), "%s: grid too large", what);
-      return launch(rt, stream, rt->k.gemm_big[t64 ? 0 : 1][rt4 ? 0 : 1][a.mode],
-                    (uint32_t)(groups * 8 * tiles), 1, 0, p, what);
+      uint32_t ksplit = 1;
+      while (ksplit < kmax && wgs(t64, rt4) * ksplit < need) ksplit *= 2;
+      if (ksplit > 1) {
+        p.ws = (float *)a.ws;
+        p.ksplit = ksplit;
+        p.kchunks = cdiv(chunks, ksplit);
+      }
+      AMMON_CHECK(groups * 8 * tiles * ksplit < (1ull << 31), "%s: grid too large", what);
+      ammon_status st = launch(rt, stream, rt->k.gemm_big[t64 ? 0 : 1][rt4 ? 0 : 1][a.mode],
+                               (uint32_t)(groups * 8 * tiles * ksplit), 1, 0, p, what);
+      if (st != AMMON_OK || ksplit == 1) return st;
+      const uint64_t elems = (uint64_t)a.tokens * a.d;
+      const uint32_t blocks = (uint32_t)std::min<uint64_t>(cdiv(elems, kWorkgroup), cus * 4ull);
+      return launch(rt, stream, rt->k.gemm_reduce, blocks, 1, 0, p, what);
     }
   }
   // 64 virtual rows x 16 tokens per workgroup for short prompts, x 32 beyond;
@@ -550,9 +591,20 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
 
 }  // namespace
 
+size_t ammon_prefill_gemm_workspace_bytes(uint32_t d, uint32_t tokens) {
+  return (size_t)8 * tokens * d * sizeof(float);
+}
+
 ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const void *w,
                                 ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
                                 uint32_t tokens, float *y, const float *residual) {
+  return ammon_prefill_gemm_ws(rt, stream, w, w_dtype, d, n, x, tokens, y, residual, nullptr, 0);
+}
+
+ammon_status ammon_prefill_gemm_ws(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                   ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                   uint32_t tokens, float *y, const float *residual,
+                                   void *workspace, size_t workspace_bytes) {
   REQUIRE_RT();
   GemmArgs a = {};
   a.mode = residual ? AMMON_GEMV_RESIDUAL : AMMON_GEMV_PLAIN;
@@ -566,6 +618,8 @@ ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const vo
   a.residual = residual;
   a.y = y;
   a.y_bytes = (size_t)tokens * d * 4;
+  a.ws = workspace;
+  a.ws_bytes = workspace ? workspace_bytes : 0;
   return gemm_check_and_launch(rt, stream, a, "prefill_gemm");
 }
 

@@ -153,6 +153,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
                    s ? "_k4" : "");
           R(7, name, k.gemm[d][t][s][m]);
         }
+  R(7, "ammon_gemm_reduce", k.gemm_reduce);
   for (int t = 0; t < 2; ++t)
     for (int r = 0; r < 2; ++r)
       for (int m = 0; m < kGemvModes; ++m) {

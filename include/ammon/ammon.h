@@ -313,6 +313,18 @@ ammon_status ammon_greedy_lm_head(ammon_runtime *rt, ammon_stream stream, const 
 ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const void *w,
                                 ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
                                 uint32_t tokens, float *y, const float *residual);
+/* ammon_prefill_gemm with a workspace of workspace_bytes (16-byte aligned,
+ * not overlapping x, y or residual): with bf16 weights, projections whose
+ * tiles alone would leave CUs idle (few rows, a long reduction, a short
+ * prompt) split the reduction into ranges whose partial sums go to the
+ * workspace and are added in range order by a second launch -- the result
+ * is deterministic.  ammon_prefill_gemm_workspace_bytes gives the size that
+ * allows every split. */
+size_t ammon_prefill_gemm_workspace_bytes(uint32_t d, uint32_t tokens);
+ammon_status ammon_prefill_gemm_ws(ammon_runtime *rt, ammon_stream stream, const void *w,
+                                   ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
+                                   uint32_t tokens, float *y, const float *residual,
+                                   void *workspace, size_t workspace_bytes);
 /* ammon_qkv_rope_store over rows of an already normalised x: q [tokens,
  * q_heads * head]; rotated k and raw v rows go to the caches at positions
  * step->position + t.  head a multiple of 16. */

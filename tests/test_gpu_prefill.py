@@ -80,6 +80,35 @@ def test_prefill_gemm_matches_oracle_gemv(rt, d, n, tokens, w_dtype):
     assert rel_err(r.download((tokens, d)), rh + want) <= RTOL
 
 
+@pytest.mark.parametrize("d,n,tokens", [(1024, 8192, 64), (520, 4104, 100), (256, 2048, 40)])
+def test_prefill_gemm_split_reduction(rt, d, n, tokens):
+    """With a workspace, few-row projections split the reduction into ranges
+    summed in order by a second launch: oracle parity, the residual form in
+    place, repeatable to the bit, and equal within rounding to the unsplit
+    GEMM."""
+    wh = oracle.storage(oracle.normal(d * n, 205, std=0.02), BF16).reshape(d, n)
+    xh = oracle.normal(tokens * n, 206).reshape(tokens, n)
+    w, x = up(rt, wh), up(rt, xh)
+    nbytes = _abi.lib.ammon_prefill_gemm_workspace_bytes(d, tokens)
+    assert nbytes == 8 * tokens * d * 4
+    ws = rt.alloc(nbytes)
+    want = np.stack([oracle.gemv(wh, BF16, xh[t]) for t in range(tokens)])
+    y1, y2, y0 = rt.alloc(tokens * d * 4), rt.alloc(tokens * d * 4), rt.alloc(tokens * d * 4)
+    for y in (y1, y2):
+        call("ammon_prefill_gemm_ws", rt.handle, None, w, BF16, d, n, x, tokens, y, None, ws, nbytes)
+    call("ammon_prefill_gemm", rt.handle, None, w, BF16, d, n, x, tokens, y0, None)
+    g1, g2, g0 = (b.download((tokens, d)) for b in (y1, y2, y0))
+    np.testing.assert_array_equal(g1.view(np.uint32), g2.view(np.uint32))
+    assert rel_err(g1, want) <= RTOL and rel_err(g1, g0) <= RTOL
+    rh = oracle.normal(tokens * d, 207).reshape(tokens, d)
+    r = up(rt, rh)
+    call("ammon_prefill_gemm_ws", rt.handle, None, w, BF16, d, n, x, tokens, r, r, ws, nbytes)
+    assert rel_err(r.download((tokens, d)), rh + want) <= RTOL
+    with pytest.raises(AmmonError, match="workspace overlaps"):
+        call("ammon_prefill_gemm_ws", rt.handle, None, w, BF16, d, n, x, tokens, y1, None, y1,
+             nbytes)
+
+
 def test_prefill_gemm_identity_is_exact(rt):
     # the reference's identity GEMV (tests/kernels.rs:83-97) per row: exact
     for w_dtype in (F32, BF16):
