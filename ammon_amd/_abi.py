@@ -106,6 +106,8 @@ SIGNATURES = {
     "ammon_prefill_gemm": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P, _P]),
     "ammon_prefill_gemm_workspace_bytes": (_SZ, [_U32, _U32]),
     "ammon_prefill_gemm_ws": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P, _P, _P, _SZ]),
+    "ammon_prefill_qkv_rope_store_ws": (_ST, [_P, _P, _P, _U32, _P, _P, _P, _DT, _U32, _U32, _U32,
+                                              _U32, _P, _P, _P, _DT, _U32, _P, _P, _P, _SZ]),
     "ammon_prefill_qkv_rope_store": (_ST, [_P, _P, _P, _U32, _P, _P, _P, _DT, _U32, _U32, _U32,
                                            _U32, _P, _P, _P, _DT, _U32, _P, _P]),
     "ammon_prefill_gate_up_swiglu": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _P]),

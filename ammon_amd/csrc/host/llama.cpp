@@ -507,9 +507,10 @@ void LlamaModel::ensure_prefill(uint32_t n) {
   pf_q_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
   pf_att_ = Tensor::zeros(rt_, Shape::from_dims({cap, q_dim_}), DType::F32);
   pf_hb_ = Tensor::zeros(rt_, Shape::from_dims({cap, c_.hidden}), DType::F32);
-  // split-reduction partial sums of the wo and w2 GEMMs ([tokens, dim] outputs)
+  // split-reduction partial sums of the QKV, wo and w2 GEMMs
+  const uint32_t ws_rows = std::max(c_.dim, q_dim_ + 2 * c_.n_kv_heads * head_);
   pf_ws_ = Tensor::zeros(
-      rt_, Shape::vector((uint32_t)(ammon_prefill_gemm_workspace_bytes(c_.dim, cap) / 4)),
+      rt_, Shape::vector((uint32_t)(ammon_prefill_gemm_workspace_bytes(ws_rows, cap) / 4)),
       DType::F32);
   pf_cap_ = cap;
 }
@@ -558,9 +559,10 @@ void LlamaModel::prefill(const int32_t *tokens, uint32_t n, uint32_t start, floa
     KvLayer kv = cache_.layer(l);
     check(ammon_rmsnorm(rt, st, x, aw.norm.data(), AMMON_F32, xn, n, c_.dim, c_.eps),
           "prefill rmsnorm");
-    check(ammon_prefill_qkv_rope_store(rt, st, xn, n, aw.query.data(), aw.key.data(), aw.value.data(), wd,
-                                       c_.dim, c_.n_heads, c_.n_kv_heads, head_, q, kv.key.data(),
-                                       kv.value.data(), kvd, c_.max_seq, step, table),
+    check(ammon_prefill_qkv_rope_store_ws(rt, st, xn, n, aw.query.data(), aw.key.data(),
+                                          aw.value.data(), wd, c_.dim, c_.n_heads, c_.n_kv_heads,
+                                          head_, q, kv.key.data(), kv.value.data(), kvd,
+                                          c_.max_seq, step, table, pf_ws_.data(), pf_ws_.nbytes()),
           "prefill qkv");
     check(ammon_attention_prefill(rt, st, q, n, c_.n_heads, kv.key.data(), kv.value.data(), kvd,
                                   c_.n_kv_heads, head_, c_.max_seq, step, ctx, split,

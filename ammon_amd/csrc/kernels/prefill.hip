@@ -388,6 +388,42 @@ AMMON_DEV void gemm(const ammon_k_gemm &p) {
   tile.epilogue(acc, xs);
 }
 
+// QKV epilogue of virtual rows (v, v + 1) of token t: rotate q and k pairs
+// with the cos/sin table at position step->position + t; q to y, k and raw
+// v rows to the head-major caches (src/kernels.rs:174-226); a position past
+// the cache poisons q and touches no cache.
+AMMON_DEV void qkv_store_pair(const ammon_k_gemm &p, uint32_t t, uint32_t v, float a0, float a1) {
+#pragma clang fp contract(off)
+  const uint32_t pos = p.step->position + t;
+  const uint32_t kvd = p.kv_dim;
+  if (pos >= p.seq) {
+    if (v < p.d) {
+      p.y[(size_t)t * p.d + v] = __uint_as_float(0x7fc00000u);
+      p.y[(size_t)t * p.d + v + 1] = __uint_as_float(0x7fc00000u);
+    }
+    return;
+  }
+  if (v < p.d + kvd) {
+    const uint32_t rr = v < p.d ? v : v - p.d;
+    const uint32_t hd = rr % p.head;
+    const float *cs = p.table + ((size_t)pos * (p.head / 2) + hd / 2) * 2;
+    const float fcr = cs[0], fci = cs[1];
+    const float o0 = a0 * fcr - a1 * fci;
+    const float o1 = a0 * fci + a1 * fcr;
+    if (v < p.d) {
+      p.y[(size_t)t * p.d + v] = o0;
+      p.y[(size_t)t * p.d + v + 1] = o1;
+    } else {
+      store_pair_out(p.k_cache, p.kv_dtype, ((size_t)(rr / p.head) * p.seq + pos) * p.head + hd,
+                     o0, o1);
+    }
+  } else {
+    const uint32_t rv = v - p.d - kvd;
+    store_pair_out(p.v_cache, p.kv_dtype,
+                   ((size_t)(rv / p.head) * p.seq + pos) * p.head + rv % p.head, a0, a1);
+  }
+}
+
 // ---- long prompts: register-blocked tiles ----------------------------------
 // For prompts of 64 tokens and more a workgroup owns 64 tokens (4 column
 // tiles) x 4 waves x RT 16-row tiles per wave.  Every B fragment (x part)
@@ -536,8 +572,8 @@ struct BigTile {
     for (uint32_t c = 0; c < NT; ++c) {
       const uint32_t t = tok0 + 16 * c + (lane & 15);
       if (t >= p.tokens) continue;
-      if ((MODE == AMMON_GEMV_PLAIN || MODE == AMMON_GEMV_RESIDUAL) && p.ksplit > 1) {
-        float *w = p.ws + ((size_t)ks * p.tokens + t) * p.d;  // this range's partial sums
+      if (MODE != AMMON_GEMV_SWIGLU && p.ksplit > 1) {
+        float *w = p.ws + ((size_t)ks * p.tokens + t) * p.rows;  // this range's partial sums
 #pragma unroll
         for (uint32_t j = 0; j < RT; ++j)
 #pragma unroll
@@ -558,42 +594,12 @@ struct BigTile {
             p.y[(size_t)t * p.d + h] = v;
           }
       } else if (MODE == AMMON_GEMV_QKV) {
-#pragma clang fp contract(off)
-        const uint32_t pos = p.step->position + t;
-        const uint32_t kvd = p.kv_dim;
 #pragma unroll
         for (uint32_t j = 0; j < RT; ++j)
 #pragma unroll
           for (int i = 0; i < 4; i += 2) {
             const uint32_t v = vr[j] + rq + i;
-            if (v >= p.rows) continue;
-            const float a0 = acc[j][c][i], a1 = acc[j][c][i + 1];
-            if (pos >= p.seq) {  // out-of-range position: poison q, touch no cache
-              if (v < p.d) {
-                p.y[(size_t)t * p.d + v] = __uint_as_float(0x7fc00000u);
-                p.y[(size_t)t * p.d + v + 1] = __uint_as_float(0x7fc00000u);
-              }
-              continue;
-            }
-            if (v < p.d + kvd) {
-              const uint32_t rr = v < p.d ? v : v - p.d;
-              const uint32_t hd = rr % p.head;
-              const float *cs = p.table + ((size_t)pos * (p.head / 2) + hd / 2) * 2;
-              const float fcr = cs[0], fci = cs[1];
-              const float o0 = a0 * fcr - a1 * fci;
-              const float o1 = a0 * fci + a1 * fcr;
-              if (v < p.d) {
-                p.y[(size_t)t * p.d + v] = o0;
-                p.y[(size_t)t * p.d + v + 1] = o1;
-              } else {
-                store_pair_out(p.k_cache, p.kv_dtype,
-                               ((size_t)(rr / p.head) * p.seq + pos) * p.head + hd, o0, o1);
-              }
-            } else {
-              const uint32_t rv = v - p.d - kvd;
-              store_pair_out(p.v_cache, p.kv_dtype,
-                             ((size_t)(rv / p.head) * p.seq + pos) * p.head + rv % p.head, a0, a1);
-            }
+            if (v < p.rows) qkv_store_pair(p, t, v, acc[j][c][i], acc[j][c][i + 1]);
           }
       } else {
 #pragma unroll
@@ -725,5 +731,23 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_gemm_reduce(ammon_k
     float acc = p.ws[i];
     for (uint32_t s = 1; s < p.ksplit; ++s) acc = acc + p.ws[s * total + i];
     p.y[i] = p.residual ? p.residual[i] + acc : acc;
+  }
+}
+
+// QKV: each (token, row pair) sums its split partial sums in range order,
+// then the QKV epilogue: grid-stride over tokens x rows / 2.
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_gemm_reduce_qkv(ammon_k_gemm p) {
+  const uint32_t pairs = p.rows / 2;
+  const size_t total = (size_t)p.tokens * p.rows, n = (size_t)p.tokens * pairs;
+  for (size_t i = (size_t)blockIdx.x * AMMON_WG + threadIdx.x; i < n;
+       i += (size_t)gridDim.x * AMMON_WG) {
+    const uint32_t t = (uint32_t)(i / pairs), v = 2 * (uint32_t)(i % pairs);
+    const size_t at = (size_t)t * p.rows + v;
+    float a0 = p.ws[at], a1 = p.ws[at + 1];
+    for (uint32_t s = 1; s < p.ksplit; ++s) {
+      a0 = a0 + p.ws[s * total + at];
+      a1 = a1 + p.ws[s * total + at + 1];
+    }
+    qkv_store_pair(p, t, v, a0, a1);
   }
 }

@@ -45,7 +45,8 @@ struct Kernels {
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]
   // [row tile per wave / split over the workgroup's waves][mode]
   hipFunction_t gemm[2][2][2][kGemvModes] = {};
-  hipFunction_t gemm_reduce = nullptr;  // split-reduction sum
+  hipFunction_t gemm_reduce = nullptr;      // split-reduction sum
+  hipFunction_t gemm_reduce_qkv = nullptr;  // ... with the QKV epilogue
   // bf16, register-blocked tiles: [64 tokens, 32 tokens][RT 4, RT 2][mode]
   hipFunction_t gemm_big[2][2][kGemvModes] = {};
 };

@@ -522,14 +522,13 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
       return (uint64_t)cdiv(covered, rt4 ? per4 : per4 / 2) * cdiv(a.tokens, t64 ? 64 : 32);
     };
     const uint32_t chunks = (uint32_t)cdiv(a.n, 64);
-    const bool splittable =
-        a.ws && (a.mode == AMMON_GEMV_PLAIN || a.mode == AMMON_GEMV_RESIDUAL);
+    const bool splittable = a.ws && a.mode != AMMON_GEMV_SWIGLU;
     // the most ranges of at least `len` chunks the workspace holds
     auto kmax_of = [&](uint32_t len) {
       uint32_t k = 1;
       if (splittable)
         while (k < 8 && chunks / (k * 2) >= len &&
-               (uint64_t)k * 2 * a.tokens * a.d * 4 <= a.ws_bytes)
+               (uint64_t)k * 2 * a.tokens * a.rows * 4 <= a.ws_bytes)
           k *= 2;
       return k;
     };
@@ -566,9 +565,12 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
       ammon_status st = launch(rt, stream, rt->k.gemm_big[t64 ? 0 : 1][rt4 ? 0 : 1][a.mode],
                                (uint32_t)(groups * 8 * tiles * ksplit), 1, 0, p, what);
       if (st != AMMON_OK || ksplit == 1) return st;
-      const uint64_t elems = (uint64_t)a.tokens * a.d;
+      // the ranges' sums (QKV: per row pair, then the rotation and stores)
+      const bool qkv = a.mode == AMMON_GEMV_QKV;
+      const uint64_t elems = (uint64_t)a.tokens * (qkv ? a.rows / 2 : a.d);
       const uint32_t blocks = (uint32_t)std::min<uint64_t>(cdiv(elems, kWorkgroup), cus * 4ull);
-      return launch(rt, stream, rt->k.gemm_reduce, blocks, 1, 0, p, what);
+      return launch(rt, stream, qkv ? rt->k.gemm_reduce_qkv : rt->k.gemm_reduce, blocks, 1, 0, p,
+                    what);
     }
   }
   // 64 virtual rows x 16 tokens per workgroup for short prompts, x 32 beyond;
@@ -591,8 +593,8 @@ ammon_status gemm_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
 
 }  // namespace
 
-size_t ammon_prefill_gemm_workspace_bytes(uint32_t d, uint32_t tokens) {
-  return (size_t)8 * tokens * d * sizeof(float);
+size_t ammon_prefill_gemm_workspace_bytes(uint32_t rows, uint32_t tokens) {
+  return (size_t)8 * tokens * rows * sizeof(float);
 }
 
 ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const void *w,
@@ -630,6 +632,19 @@ ammon_status ammon_prefill_qkv_rope_store(ammon_runtime *rt, ammon_stream stream
                                           float *q, void *k_cache, void *v_cache,
                                           ammon_dtype kv_dtype, uint32_t seq,
                                           const ammon_decode_step *step, const float *table) {
+  return ammon_prefill_qkv_rope_store_ws(rt, stream, x, tokens, wq, wk, wv, w_dtype, dim, q_heads,
+                                         kv_heads, head, q, k_cache, v_cache, kv_dtype, seq, step,
+                                         table, nullptr, 0);
+}
+
+ammon_status ammon_prefill_qkv_rope_store_ws(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *wq, const void *wk,
+                                          const void *wv, ammon_dtype w_dtype, uint32_t dim,
+                                          uint32_t q_heads, uint32_t kv_heads, uint32_t head,
+                                          float *q, void *k_cache, void *v_cache,
+                                          ammon_dtype kv_dtype, uint32_t seq,
+                                          const ammon_decode_step *step, const float *table,
+                                             void *workspace, size_t workspace_bytes) {
   REQUIRE_RT();
   AMMON_CHECK(wq && wk && wv, "prefill_qkv: NULL wq, wk or wv");
   AMMON_CHECK(k_cache && v_cache && step && table, "prefill_qkv: NULL cache, step or table");
@@ -664,6 +679,12 @@ ammon_status ammon_prefill_qkv_rope_store(ammon_runtime *rt, ammon_stream stream
   a.head = head;
   a.seq = seq;
   a.kv_dtype = kv_dtype;
+  a.ws = workspace;
+  a.ws_bytes = workspace ? workspace_bytes : 0;
+  const size_t cache_bytes = (size_t)kv_dim * seq * dsize(kv_dtype);
+  AMMON_CHECK(!workspace || (!overlaps(workspace, workspace_bytes, k_cache, cache_bytes) &&
+                             !overlaps(workspace, workspace_bytes, v_cache, cache_bytes)),
+              "prefill_qkv: workspace overlaps a cache");
   return gemm_check_and_launch(rt, stream, a, "prefill_qkv_rope_store");
 }
 

@@ -154,6 +154,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
           R(7, name, k.gemm[d][t][s][m]);
         }
   R(7, "ammon_gemm_reduce", k.gemm_reduce);
+  R(7, "ammon_gemm_reduce_qkv", k.gemm_reduce_qkv);
   for (int t = 0; t < 2; ++t)
     for (int r = 0; r < 2; ++r)
       for (int m = 0; m < kGemvModes; ++m) {

@@ -318,9 +318,10 @@ ammon_status ammon_prefill_gemm(ammon_runtime *rt, ammon_stream stream, const vo
  * tiles alone would leave CUs idle (few rows, a long reduction, a short
  * prompt) split the reduction into ranges whose partial sums go to the
  * workspace and are added in range order by a second launch -- the result
- * is deterministic.  ammon_prefill_gemm_workspace_bytes gives the size that
- * allows every split. */
-size_t ammon_prefill_gemm_workspace_bytes(uint32_t d, uint32_t tokens);
+ * is deterministic.  ammon_prefill_gemm_workspace_bytes(rows, tokens) gives
+ * the size that allows every split (rows = d here; (q_heads + 2 kv_heads)
+ * head for ammon_prefill_qkv_rope_store_ws). */
+size_t ammon_prefill_gemm_workspace_bytes(uint32_t rows, uint32_t tokens);
 ammon_status ammon_prefill_gemm_ws(ammon_runtime *rt, ammon_stream stream, const void *w,
                                    ammon_dtype w_dtype, uint32_t d, uint32_t n, const float *x,
                                    uint32_t tokens, float *y, const float *residual,
@@ -335,6 +336,15 @@ ammon_status ammon_prefill_qkv_rope_store(ammon_runtime *rt, ammon_stream stream
                                           float *q, void *k_cache, void *v_cache,
                                           ammon_dtype kv_dtype, uint32_t seq,
                                           const ammon_decode_step *step, const float *table);
+/* ... with a workspace for a split reduction, as ammon_prefill_gemm_ws. */
+ammon_status ammon_prefill_qkv_rope_store_ws(ammon_runtime *rt, ammon_stream stream, const float *x,
+                                          uint32_t tokens, const void *wq, const void *wk,
+                                          const void *wv, ammon_dtype w_dtype, uint32_t dim,
+                                          uint32_t q_heads, uint32_t kv_heads, uint32_t head,
+                                          float *q, void *k_cache, void *v_cache,
+                                          ammon_dtype kv_dtype, uint32_t seq,
+                                          const ammon_decode_step *step, const float *table,
+                                             void *workspace, size_t workspace_bytes);
 /* ammon_gate_up_swiglu over rows of an already normalised x: hb [tokens,
  * hidden]. */
 ammon_status ammon_prefill_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const float *x,

@@ -151,7 +151,10 @@ def test_prefill_gate_up_swiglu(rt, dim, hidden, tokens, w_dtype):
 
 @pytest.mark.parametrize("shape", ["c1", "c4", "c4_long"])
 @pytest.mark.parametrize("kv_dtype", [F32, BF16])
-def test_prefill_qkv_rope_store(rt, shape, kv_dtype):
+@pytest.mark.parametrize("use_ws", [False, True])
+def test_prefill_qkv_rope_store(rt, shape, kv_dtype, use_ws):
+    """use_ws: the workspace entry, whose c4 shape (6144 rows, 40 tokens)
+    splits the reduction and rotates / stores in the summing launch."""
     if shape == "c1":
         dim, q_heads, kv_heads, head, seq, w_dtype, theta, p0, T = 288, 6, 6, 48, 64, F32, 1e4, 0, 9
     elif shape == "c4":
@@ -176,8 +179,15 @@ def test_prefill_qkv_rope_store(rt, shape, kv_dtype):
     vc = up(rt, np.zeros((kv_heads, seq, head), npdt(kv_dtype)))
     x, q, table = up(rt, xh), rt.alloc(T * qd * 4), up(rt, table_h)
     step = rt.step(0, p0)
-    call("ammon_prefill_qkv_rope_store", rt.handle, None, x, T, up(rt, wq), up(rt, wk), up(rt, wv),
-         w_dtype, dim, q_heads, kv_heads, head, q, kc, vc, kv_dtype, seq, step, table)
+    if use_ws:
+        nbytes = _abi.lib.ammon_prefill_gemm_workspace_bytes(qd + 2 * kd, T)
+        call("ammon_prefill_qkv_rope_store_ws", rt.handle, None, x, T, up(rt, wq), up(rt, wk),
+             up(rt, wv), w_dtype, dim, q_heads, kv_heads, head, q, kc, vc, kv_dtype, seq, step,
+             table, rt.alloc(nbytes), nbytes)
+    else:
+        call("ammon_prefill_qkv_rope_store", rt.handle, None, x, T, up(rt, wq), up(rt, wk),
+             up(rt, wv), w_dtype, dim, q_heads, kv_heads, head, q, kc, vc, kv_dtype, seq, step,
+             table)
     assert rel_err(q.download((T, qd)), want_q) <= RTOL
     got_k = pos_major(kc.download((kv_heads, seq, head), npdt(kv_dtype)), kv_heads, seq, head)
     got_v = pos_major(vc.download((kv_heads, seq, head), npdt(kv_dtype)), kv_heads, seq, head)
