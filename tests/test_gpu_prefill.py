@@ -109,6 +109,34 @@ def test_prefill_gemm_split_reduction(rt, d, n, tokens):
              nbytes)
 
 
+def test_prefill_gemm_random_shapes(rt):
+    """Seeded random shapes through every tile family and the split
+    reduction (rows, reduction length and tokens off every tile multiple),
+    bf16 weights, with and without a workspace, against the oracle."""
+    rng = np.random.default_rng(12)
+    for case in range(16):
+        d = int(rng.integers(1, 700))
+        n = 8 * int(rng.integers(1, 700))
+        tokens = int(rng.choice([1, 3, 16, 17, 31, 33, 63, 64, 65, 100, 130]))
+        wh = oracle.storage(oracle.normal(d * n, 300 + case, std=0.05), BF16).reshape(d, n)
+        xh = oracle.normal(tokens * n, 400 + case).reshape(tokens, n)
+        rh = oracle.normal(tokens * d, 500 + case).reshape(tokens, d)
+        want = np.stack([oracle.gemv(wh, BF16, xh[t]) for t in range(tokens)])
+        w, x = up(rt, wh), up(rt, xh)
+        nbytes = _abi.lib.ammon_prefill_gemm_workspace_bytes(d, tokens)
+        ws = rt.alloc(nbytes)
+        for use_ws in (False, True):
+            r = up(rt, rh)
+            if use_ws:
+                call("ammon_prefill_gemm_ws", rt.handle, None, w, BF16, d, n, x, tokens, r, r, ws,
+                     nbytes)
+            else:
+                call("ammon_prefill_gemm", rt.handle, None, w, BF16, d, n, x, tokens, r, r)
+            # the projection part (y - residual: exact but for y's rounding)
+            got = r.download((tokens, d)).astype(np.float64) - rh
+            assert rel_err(got, want) <= 2 * RTOL, (d, n, tokens, use_ws)
+
+
 def test_prefill_gemm_identity_is_exact(rt):
     # the reference's identity GEMV (tests/kernels.rs:83-97) per row: exact
     for w_dtype in (F32, BF16):
