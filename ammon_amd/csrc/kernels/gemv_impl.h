@@ -187,7 +187,28 @@ struct GemvPass {
     const bool xvec = (n & 3u) == 0 && (((uintptr_t)p.x) & 15u) == 0;
     const bool wvec = p.norm_w == nullptr || p.norm_dtype == AMMON_K_BF16 ||
                       (((uintptr_t)p.norm_w) & 15u) == 0;
-    if (xvec && wvec && n / 4 <= XREG * AMMON_WG) {
+    if (!p.norm_w && xvec && n / 4 > XREG * AMMON_WG) {
+      // Long x without a norm (the down projection): 16-byte buffer loads
+      // straight into LDS, all of a wave's in flight at once and no
+      // registers held (the register loop below waits once per four
+      // quads); quads past n read as zero.  Wave w fills groups w, w + 4,
+      // ... of GQ quads: with 8-element chunks the two planes of a group
+      // are two loads (even quads, then odd), each lane's 16 bytes landing
+      // at slot lane of its plane.
+      const __amdgpu_buffer_rsrc_t xres = make_rsrc(p.x, n * 4u);
+      constexpr uint32_t GQ = CH == 8 ? 128 : 64;
+      const uint32_t groups = tiles * tile_chunks * CH / 4 / GQ;
+      for (uint32_t g = wave_u; g < groups; g += AMMON_WAVES) {
+#pragma unroll
+        for (uint32_t pl = 0; pl < GQ / 64; ++pl) {
+          const uint32_t q = g * GQ + (GQ == 128 ? 2 * lane + pl : lane);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xres, (__attribute__((address_space(3))) void *)(xs4 + g * GQ + pl * 64), 16,
+              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, 0);
+        }
+      }
+      __builtin_amdgcn_s_waitcnt(0);
+    } else if (xvec && wvec && n / 4 <= XREG * AMMON_WG) {
       float4 xr[XREG], wr[XREG];
       float ss = 0.f;
 #pragma unroll
