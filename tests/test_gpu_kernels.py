@@ -372,8 +372,11 @@ def test_matmul_identity(rt):
         np.testing.assert_array_equal(down(y, 2), xv)
 
 
+# n > 4096 without a norm stages x by direct-to-LDS loads: whole and ragged
+# tiles for 8-wide (bf16), 4-wide (fp32) and 1-wide chunks (bf16, n % 8 = 4)
 GEMV_SHAPES = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336), (288, 288), (768, 288),
-               (288, 768), (7, 5), (33, 300), (1, 1), (5, 4100)]
+               (288, 768), (7, 5), (33, 300), (1, 1), (5, 4100), (17, 5000), (9, 8200),
+               (3, 12292)]
 
 
 @pytest.mark.parametrize("d,n", GEMV_SHAPES)
