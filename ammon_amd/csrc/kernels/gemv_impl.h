@@ -197,6 +197,7 @@ struct GemvPass {
       // at slot lane of its plane.
       const __amdgpu_buffer_rsrc_t xres = make_rsrc(p.x, n * 4u);
       constexpr uint32_t GQ = CH == 8 ? 128 : 64;
+      static_assert(tile_chunks * CH / 4 % GQ == 0, "whole groups per tile");
       const uint32_t groups = tiles * tile_chunks * CH / 4 / GQ;
       for (uint32_t g = wave_u; g < groups; g += AMMON_WAVES) {
 #pragma unroll
