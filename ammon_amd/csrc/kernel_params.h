@@ -144,6 +144,12 @@ typedef struct {
 } ammon_k_argmax;
 
 typedef struct {
+  const void *src;          /* bytes, a multiple of 8, 16-byte aligned */
+  uint64_t bytes;
+  unsigned long long *out;  /* [2]: wrapping sum, xor of the 64-bit words; zeroed first */
+} ammon_k_checksum;
+
+typedef struct {
   void *dst;
   uint64_t count, seed, stream;
   float mean, std;

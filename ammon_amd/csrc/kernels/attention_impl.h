@@ -105,8 +105,9 @@ struct AttnPartial {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const uint32_t off = off_of(c0 + r * round + wave * PW + slot);
-      kr[r] = C::load_buf(kres, off);
-      vr[r] = C::load_buf(vres, off);
+      // the row at the position may have been stored earlier in this launch
+      kr[r] = C::template load_buf<AMMON_HANDOFF_CPOL>(kres, off);
+      vr[r] = C::template load_buf<AMMON_HANDOFF_CPOL>(vres, off);
     }
   }
 
@@ -148,7 +149,7 @@ struct AttnPartial {
 #pragma unroll
       for (int c = 0; c < CH; c += QCH) {
         float f[QCH];
-        QC::widen(ok ? QC::load(qp + c) : QC::zero(), f);
+        QC::widen(ok ? QC::load_in(qp + c) : QC::zero(), f);
 #pragma unroll
         for (int e = 0; e < QCH; ++e) qr[j][c + e] = f[e];
       }
@@ -327,13 +328,13 @@ struct AttnPartialMfma {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
       const uint32_t off = tk < n ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
-      kr[kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, 0);
+      kr[kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, AMMON_HANDOFF_CPOL);
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t tv = c0 + 16 * wave + 4 * k + (lane >> 4);
       const uint32_t off = tv < n ? (tv * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
-      vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, 0);
+      vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, AMMON_HANDOFF_CPOL);
     }
   }
 
@@ -357,8 +358,8 @@ struct AttnPartialMfma {
       const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
 #pragma unroll
       for (int kk = 0; kk < 4; ++kk) {
-        qraw[kk][0] = ok ? *(const float4 *)(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-        qraw[kk][1] = ok ? *(const float4 *)(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qraw[kk][0] = ok ? ld_in4(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+        qraw[kk][1] = ok ? ld_in4(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
 #pragma unroll
@@ -580,12 +581,12 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     for (int r = 0; r < COMB_ROUNDS; ++r) {
       const uint32_t s = sl + r * COMB_SPLIT_LANES;
       const float *row = base + (size_t)(s < live ? s : 0) * slot;
-      mv[r] = s < live ? row[head] : -INFINITY;
-      lv[r] = row[head + 1];
+      mv[r] = s < live ? ld_in(row + head) : -INFINITY;
+      lv[r] = ld_in(row + head + 1);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t d = d0 + dq + k;
-        dv[r][k] = d < head ? row[d] : 0.f;
+        dv[r][k] = d < head ? ld_in(row + d) : 0.f;
       }
     }
     float m = mv[0];
@@ -602,16 +603,17 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     }
   } else {
     float m = -INFINITY;
-    for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG) m = fmaxf(m, base[(size_t)s * slot + head]);
+    for (uint32_t s = threadIdx.x; s < live; s += AMMON_WG)
+      m = fmaxf(m, ld_in(base + (size_t)s * slot + head));
     const float M = block_max(m, red);
     for (uint32_t s = sl; s < live; s += COMB_SPLIT_LANES) {
       const float *row = base + (size_t)s * slot;
-      const float w = expf(row[head] - M);
-      if ((threadIdx.x & 3) == 0) l = fmaf(row[head + 1], w, l);
+      const float w = expf(ld_in(row + head) - M);
+      if ((threadIdx.x & 3) == 0) l = fmaf(ld_in(row + head + 1), w, l);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {
         const uint32_t d = d0 + dq + k;
-        if (d < head) a[k] = fmaf(row[d], w, a[k]);
+        if (d < head) a[k] = fmaf(ld_in(row + d), w, a[k]);
       }
     }
   }

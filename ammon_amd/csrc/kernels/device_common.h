@@ -31,23 +31,49 @@ AMMON_DEV void store_elem(void *base, uint32_t dtype, size_t i, float v) {
     ((float *)base)[i] = v;
 }
 
-// Output stores (activations, K/V rows, attention partials).  A code object
-// that hands results to other workgroups inside one launch (the persistent
-// token kernel) defines AMMON_AGENT_STORES to 1 before including this
-// header: its outputs are then stored at agent scope (global_store ... sc1),
-// written through to the device coherence point, so another XCD that has
-// not cached the line reads the new value without any L2 writeback.
-// Standalone kernels hand results over at kernel boundaries only and use
-// plain stores, which complete at L2.
-#ifndef AMMON_AGENT_STORES
-#define AMMON_AGENT_STORES 0
+// Hand-off of results between workgroups.  Standalone kernels hand results
+// over at kernel boundaries only: plain stores (complete at L2) and plain
+// loads.  A code object whose workgroups hand results to each other inside
+// one launch (the persistent token kernel) defines AMMON_AGENT_HANDOFF to 1
+// before including this header; then
+//   - outputs (activations, K/V rows, partials, candidates) are stored at
+//     agent scope (global_store ... sc1): written through to the device
+//     coherence point, never left dirty in one XCD's L2;
+//   - every load of a value another workgroup wrote in the same launch is an
+//     agent-scope load (sc1: ld_in / ld_in4 / AMMON_HANDOFF_CPOL on buffer
+//     loads), which the memory model makes coherent per location -- it cannot
+//     return a stale line from this CU's L1 or this XCD's L2, whatever lines
+//     (shared with other slices, or cached by earlier reads) they hold.
+// A grid barrier between producer and consumer orders the two: producers
+// wait for their stores to complete (s_waitcnt) before counting in, and
+// consumers issue these loads only after the count is seen.
+#ifndef AMMON_AGENT_HANDOFF
+#define AMMON_AGENT_HANDOFF 0
 #endif
+#define AMMON_HANDOFF_CPOL (AMMON_AGENT_HANDOFF ? 16 : 0)  // buffer-load aux: sc1
 template <typename T>
 AMMON_DEV void st_out_t(T *p, T v) {
-  if (AMMON_AGENT_STORES)
+  if (AMMON_AGENT_HANDOFF)
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   else
     *p = v;
+}
+// Load of a value another workgroup may have written in this launch.
+template <typename T>
+AMMON_DEV T ld_in(const T *p) {
+  if (AMMON_AGENT_HANDOFF) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+// ... four floats at a 16-byte-aligned address (two 8-byte agent loads).
+AMMON_DEV float4 ld_in4(const float *p) {
+  if (AMMON_AGENT_HANDOFF) {
+    const uint64_t a = __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const uint64_t b =
+        __hip_atomic_load((const uint64_t *)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
+                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
+  }
+  return *(const float4 *)p;
 }
 AMMON_DEV void st_out(float *p, float v) { st_out_t(p, v); }
 AMMON_DEV void st_out(uint32_t *p, uint32_t v) { st_out_t(p, v); }
@@ -90,8 +116,9 @@ template <typename T, int CH> struct Chunk;
 
 template <> struct Chunk<uint16_t, 8> {
   using V = u32x4;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL);
   }
   static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
@@ -106,8 +133,9 @@ template <> struct Chunk<uint16_t, 8> {
 
 template <> struct Chunk<uint16_t, 4> {
   using V = u32x2;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CPOL);
   }
   static AMMON_DEV V load(const uint16_t *p) { return *(const V *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return __builtin_nontemporal_load((const V *)p); }
@@ -120,8 +148,9 @@ template <> struct Chunk<uint16_t, 4> {
 
 template <> struct Chunk<uint16_t, 2> {
   using V = uint32_t;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL);
   }
   static AMMON_DEV V load(const uint16_t *p) { return *(const uint32_t *)p; }
   static AMMON_DEV V load_nt(const uint16_t *p) {
@@ -133,8 +162,9 @@ template <> struct Chunk<uint16_t, 2> {
 
 template <> struct Chunk<uint16_t, 1> {
   using V = uint16_t;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, 0);
+    return __builtin_amdgcn_raw_buffer_load_b16(r, off, 0, CPOL);
   }
   static AMMON_DEV V load(const uint16_t *p) { return *p; }
   static AMMON_DEV V load_nt(const uint16_t *p) { return *p; }
@@ -144,10 +174,15 @@ template <> struct Chunk<uint16_t, 1> {
 
 template <> struct Chunk<float, 4> {
   using V = f32x4;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
+  static AMMON_DEV V load_in(const float *p) {  // handed-off data (ld_in4)
+    const float4 v = ld_in4(p);
+    return V{v.x, v.y, v.z, v.w};
+  }
   static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0.f, 0.f, 0.f, 0.f}; }
   static AMMON_DEV void widen(V v, float *f) { f[0] = v[0]; f[1] = v[1]; f[2] = v[2]; f[3] = v[3]; }
@@ -155,10 +190,15 @@ template <> struct Chunk<float, 4> {
 
 template <> struct Chunk<float, 2> {
   using V = f32x2;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
+  static AMMON_DEV V load_in(const float *p) {  // handed-off data (8-byte agent load)
+    const uint64_t a = ld_in((const uint64_t *)p);
+    return V{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32))};
+  }
   static AMMON_DEV V load_nt(const float *p) { return __builtin_nontemporal_load((const V *)p); }
   static AMMON_DEV V zero() { return V{0.f, 0.f}; }
   static AMMON_DEV void widen(V v, float *f) { f[0] = v[0]; f[1] = v[1]; }
@@ -166,10 +206,12 @@ template <> struct Chunk<float, 2> {
 
 template <> struct Chunk<float, 1> {
   using V = float;
+  template <int CPOL = 0>
   static AMMON_DEV V load_buf(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0));
+    return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *p; }
+  static AMMON_DEV V load_in(const float *p) { return ld_in(p); }  // handed-off data
   static AMMON_DEV V load_nt(const float *p) { return *p; }
   static AMMON_DEV V zero() { return 0.f; }
   static AMMON_DEV void widen(V v, float *f) { f[0] = v; }

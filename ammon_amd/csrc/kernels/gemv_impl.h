@@ -38,8 +38,10 @@
 // x 64*U chunks, software-pipelined through two register buffers -- the
 // next tile's loads are in flight while the current one is multiplied.
 //
-// Outputs (y, K/V rows) are stored at agent scope (st_out): a consumer on
-// another XCD reads them without an L2 writeback.
+// Outputs (y, K/V rows) go through st_out and inputs another workgroup may
+// have written (x, the residual) through ld_in: plain accesses in the
+// standalone kernels, agent-scope ones where workgroups hand results to
+// each other inside a launch (device_common.h, AMMON_AGENT_HANDOFF).
 //
 // The RMSNorm prologue sums squares with the same per-lane chunking and
 // reduction order as ammon_rmsnorm, so its normalised x matches the
@@ -115,7 +117,7 @@ struct GemvPass {
       const uint32_t vr = r0 + k;
       if (vr >= p.rows) continue;
       if (MODE == AMMON_GEMV_RESIDUAL) {
-        ea[k] = p.residual[vr];
+        ea[k] = ld_in(p.residual + vr);
       } else if (MODE == AMMON_GEMV_QKV && (k & 1) == 0 && pos < p.seq &&
                  vr < p.d + p.kv_dim) {
         const uint32_t rr = vr < p.d ? vr : vr - p.d;
@@ -205,7 +207,7 @@ struct GemvPass {
           const uint32_t q = g * GQ + (GQ == 128 ? 2 * lane + pl : lane);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               xres, (__attribute__((address_space(3))) void *)(xs4 + g * GQ + pl * 64), 16,
-              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, 0);
+              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, AMMON_HANDOFF_CPOL);
         }
       }
       __builtin_amdgcn_s_waitcnt(0);
@@ -216,7 +218,7 @@ struct GemvPass {
       for (int i = 0; i < XREG; ++i) {
         const uint32_t c = tid + i * AMMON_WG;
         if (c < n / 4) {
-          xr[i] = ((const float4 *)p.x)[c];
+          xr[i] = ld_in4(p.x + 4 * c);
           if (p.norm_w) {
             if (p.norm_dtype == AMMON_K_BF16) {
               const uint2 wb = ((const uint2 *)p.norm_w)[c];
@@ -261,7 +263,7 @@ struct GemvPass {
         // 16-byte loads, several in flight per lane
 #pragma unroll 4
         for (uint32_t c = tid; c < n / 4; c += AMMON_WG) {
-          const float4 v = ((const float4 *)p.x)[c];
+          const float4 v = ld_in4(p.x + 4 * c);
           xs4[xq(c)] = v;
           ss += v.x * v.x;
           ss += v.y * v.y;
@@ -270,7 +272,7 @@ struct GemvPass {
         }
       } else {
         for (uint32_t j = tid; j < n; j += AMMON_WG) {
-          const float v = p.x[j];
+          const float v = ld_in(p.x + j);
           xs[xi(j)] = v;
           ss += v * v;
         }

@@ -62,6 +62,50 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_argmax_final(ammon_
   }
 }
 
+// ---- storage checksum ------------------------------------------------------------
+// (wrapping sum, xor) of a buffer's little-endian 64-bit words.  Both are
+// associative and commutative, so the workgroups fold their results into
+// out[] with 64-bit atomics in any order and the answer is exact.  Each lane
+// keeps CK_U 16-byte loads in flight per sweep and does two integer ops per
+// word, so the kernel is a plain streaming read of the buffer.
+#define CK_U 8
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_checksum(ammon_k_checksum p) {
+  const u32x4 *src = (const u32x4 *)p.src;
+  const uint64_t n16 = p.bytes / 16;
+  const uint64_t stride = (uint64_t)gridDim.x * AMMON_WG;
+  unsigned long long s = 0, x = 0;
+  auto fold = [&](u32x4 v) {
+    const unsigned long long a = ((unsigned long long)v[1] << 32) | v[0];
+    const unsigned long long b = ((unsigned long long)v[3] << 32) | v[2];
+    s += a + b;
+    x ^= a ^ b;
+  };
+  uint64_t i = (uint64_t)blockIdx.x * AMMON_WG + threadIdx.x;
+  for (; i + (CK_U - 1) * stride < n16; i += CK_U * stride) {
+    u32x4 v[CK_U];
+#pragma unroll
+    for (int u = 0; u < CK_U; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < CK_U; ++u) fold(v[u]);
+  }
+  for (; i < n16; i += stride) fold(src[i]);
+  // an 8-byte tail word
+  if (blockIdx.x == 0 && threadIdx.x == 0 && (p.bytes & 8)) {
+    const unsigned long long t = ((const unsigned long long *)p.src)[p.bytes / 8 - 1];
+    s += t;
+    x ^= t;
+  }
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    s += __shfl_xor(s, off, 64);
+    x ^= __shfl_xor(x, off, 64);
+  }
+  if ((threadIdx.x & 63) == 0) {
+    atomicAdd(p.out, s);
+    atomicXor(p.out + 1, x);
+  }
+}
+
 // ---- fills -----------------------------------------------------------------
 AMMON_DEV uint64_t splitmix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;

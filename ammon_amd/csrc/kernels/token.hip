@@ -14,11 +14,22 @@
 //
 // Data between phases: every phase writes its own slice of the activation
 // buffers (per layer, per residual step) with agent-scope stores that write
-// through to the device coherence point (st_out), and no address is read
-// before it is written within a launch -- so no workgroup can hold a stale
-// cached copy, and the barrier needs no L2 writeback or invalidate (each
-// costs several microseconds across the device).  Lines cached by earlier
-// launches are invalidated at kernel start.
+// through to the device coherence point (st_out), and every read of a value
+// another workgroup produced in this launch -- x for a GEMV's LDS staging,
+// the residual, q, the K/V rows (the newest is stored by the QKV phase), the
+// split partials, the logits and the argmax candidates -- is an agent-scope
+// load (ld_in, ld_in4, AMMON_HANDOFF_CPOL; device_common.h).  Agent-scope
+// loads are coherent per location, so no L1 or L2 line -- whether cached by
+// an earlier read or shared with a neighbouring slice written by another
+// workgroup -- can supply a stale value, and the barrier needs no L2
+// writeback or invalidate (each costs several microseconds across the
+// device).  Order: a producer's waves wait for their stores to complete
+// (s_waitcnt vmcnt(0): stores are counted there and complete at the
+// coherence point) before the workgroup counts itself in; a consumer issues
+// its loads only after its poll has seen the full count (the loads follow
+// the poll loop's exit and the workgroup barrier).  Read-only inputs
+// (weights, norm weights, the RoPE table) and the DecodeStep (written by the
+// previous launch) use plain loads.
 //
 // Barrier: every wave waits for its stores to complete, thread 0 counts the
 // workgroup in one of 8 group counters (blockIdx % 8), the last arrival of
@@ -34,8 +45,8 @@
 // balance without a profiler; the stamps are a few stores per barrier).
 //
 // Requires all gridDim.x workgroups to be co-resident (cooperative launch).
-// outputs cross workgroups within the launch: agent-scope stores
-#define AMMON_AGENT_STORES 1
+// results cross workgroups within the launch: agent-scope stores and loads
+#define AMMON_AGENT_HANDOFF 1
 #include "argmax_impl.h"
 #include "attention_impl.h"
 #include "gemv_impl.h"
@@ -300,7 +311,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     float v = 0.f;
     uint32_t idx = ARGMAX_NONE;
     for (uint32_t i = lo + threadIdx.x; i < hi; i += AMMON_WG) {
-      const float xl = P.logits[i];
+      const float xl = ld_in(P.logits + i);
       if (xl == xl) cand_merge(v, idx, xl, i);
     }
     block_cand_reduce(v, idx, sv, si);
@@ -317,10 +328,11 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     // next = pos + 1 < n_prompt ? prompt[pos + 1] : argmax; tokens[pos] = next
     float v = 0.f;
     uint32_t idx = ARGMAX_NONE;
-    for (uint32_t b = threadIdx.x; b < G; b += AMMON_WG) cand_merge(v, idx, P.cand_v[b], P.cand_i[b]);
+    for (uint32_t b = threadIdx.x; b < G; b += AMMON_WG)
+      cand_merge(v, idx, ld_in(P.cand_v + b), ld_in(P.cand_i + b));
     block_cand_reduce(v, idx, sv, si);
     if (threadIdx.x == 0) {
-      const float first = P.logits[0];
+      const float first = ld_in(P.logits);
       const int32_t best = (first != first || idx == ARGMAX_NONE) ? 0 : (int32_t)idx;
       if (P.argmax_out) *P.argmax_out = best;
       const uint32_t pos = P.step->position;

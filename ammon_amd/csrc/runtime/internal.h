@@ -40,6 +40,7 @@ struct Kernels {
   hipFunction_t argmax_final = nullptr;
   hipFunction_t fill_normal = nullptr;
   hipFunction_t fill_const = nullptr;
+  hipFunction_t checksum = nullptr;
   // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
   hipFunction_t token[2][kAttGroups] = {};
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]

@@ -1007,4 +1007,22 @@ ammon_status ammon_fill_normal(ammon_runtime *rt, ammon_stream stream, void *dst
   return launch(rt, stream, rt->k.fill_normal, grid, 1, 0, p, "fill_normal");
 }
 
+ammon_status ammon_checksum(ammon_runtime *rt, ammon_stream stream, const void *src, size_t bytes,
+                            uint64_t *out) {
+  REQUIRE_RT();
+  AMMON_CHECK(out != nullptr && (bytes == 0 || src != nullptr), "checksum: NULL src or out");
+  AMMON_CHECK(bytes % 8 == 0, "checksum: %zu bytes is not a whole number of 64-bit words", bytes);
+  AMMON_CHECK(((uintptr_t)src & 15) == 0 && ((uintptr_t)out & 7) == 0,
+              "checksum: src must be 16-byte and out 8-byte aligned");
+  VALIDATE_ONLY();
+  // zero the two result words with a kernel (capturable), then fold
+  ammon_status st = ammon_fill(rt, stream, out, AMMON_F32, 4, 0.f);
+  if (st != AMMON_OK || bytes == 0) return st;
+  ammon_k_checksum p = {src, (uint64_t)bytes, (unsigned long long *)out};
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(
+      std::max<uint64_t>(cdiv(bytes / 16, (uint64_t)kWorkgroup * 8), 1),
+      (uint64_t)rt->info.compute_units * 4);
+  return launch(rt, stream, rt->k.checksum, grid, 1, 0, p, "checksum");
+}
+
 }  // extern "C"

@@ -138,6 +138,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   R(5, "ammon_argmax_final", k.argmax_final);
   R(5, "ammon_fill_normal", k.fill_normal);
   R(5, "ammon_fill_const", k.fill_const);
+  R(5, "ammon_checksum", k.checksum);
   for (int d = 0; d < 2; ++d)
     for (int g = 0; g < kAttGroups; ++g) {
       char name[96];

@@ -140,6 +140,15 @@ ammon_status ammon_fill_normal(ammon_runtime *rt, ammon_stream stream, void *dst
                                ammon_dtype dtype, size_t count, uint64_t seed,
                                uint64_t stream_id, float mean, float std);
 
+/* Storage checksum (no counterpart in the reference): out[0] = wrapping sum
+ * and out[1] = xor of the little-endian 64-bit words of src[0, bytes) (bytes
+ * a multiple of 8, src 16-byte aligned; out is 2 words of device memory).
+ * Proves two copies of a tensor identical bit for bit (device-generated
+ * weights against a host fixture) without moving them; as a plain streaming
+ * read it also gives the device's HBM read ceiling. */
+ammon_status ammon_checksum(ammon_runtime *rt, ammon_stream stream, const void *src, size_t bytes,
+                            uint64_t *out);
+
 /* ---- host utilities (no device needed) ----------------------------------- */
 
 /* RoPE cos/sin table [seq, head/2, 2] with the reference's fp32 formula

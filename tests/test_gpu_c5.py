@@ -4,9 +4,11 @@ cache) decoding at context 32768 with the cache prefilled N(0, 1): the
 device path against the oracle on the very same weights and cache.
 
 Weights and cache are generated on the device and copied to the host, so
-both sides start bit-identical.  Logits and the K/V rows the steps write
-must agree to the bf16 bar (a last-bit difference of the fp32 projection
-can flip one bf16 rounding of a cached K/V element), and the greedy token of
+both sides start bit-identical.  The only difference is the fp32 summation
+order (~4e-6 relative), which can flip the bf16 rounding of a newly stored
+K/V element by one bf16 ulp (at most 2^-7 of the element): the written rows
+must agree to 2^-7 normwise, the logits to 1e-3 normwise (the effect of
+about two flips per 1024-element row is ~3.5e-4), and the greedy token of
 every step must be the oracle's.
 """
 import ctypes
@@ -19,7 +21,8 @@ from ammon_amd import LlamaModel, kv_unpermute
 from ammon_amd._abi import BF16, F32, call
 
 pytestmark = pytest.mark.gpu
-BF16_TOL = 2e-2
+BF16_KV_TOL = 1e-3     # logits, same weights and cache, bf16 KV
+KV_STORE_TOL = 2.0**-7  # stored bf16 K/V rows: one bf16 ulp at the largest element
 
 C5 = dict(dim=8192, n_layers=1, n_heads=64, n_kv_heads=8, hidden=28672, vocab=128256,
           max_seq=32768, theta=500000.0)
@@ -72,7 +75,7 @@ def test_c5_layer_decode_at_ctx_32768(rt):
         want = om.step(tok, pos)
         err = rel_err(got, want)
         say(f"pos {pos}: logits rel err {err:.2e}")
-        assert err <= BF16_TOL, pos
+        assert err <= BF16_KV_TOL, pos
         assert np.all(np.isfinite(got))
         nxt = oracle.sample_argmax(want)
         assert oracle.sample_argmax(got) == nxt, pos
@@ -81,7 +84,7 @@ def test_c5_layer_decode_at_ctx_32768(rt):
     for got_pm, want_pm, before in zip(m.kv_layer(0), om.kv_layer(0), caches):
         rows = slice(32765, 32768)
         assert rel_err(oracle.widen(got_pm[rows], BF16), oracle.widen(want_pm[rows], BF16)) \
-            <= BF16_TOL
+            <= KV_STORE_TOL
         np.testing.assert_array_equal(got_pm[:32765], before[:32765])
     om.close()
     m.close()

@@ -559,6 +559,25 @@ def test_fill_normal_matches_oracle_generator(rt, dtype):
     assert np.mean(got != want) < 1e-5
 
 
+@pytest.mark.parametrize("nbytes", [0, 8, 24, 4096, (1 << 22) + 8, (3 << 24) + 48])
+def test_checksum_matches_numpy(rt, nbytes):
+    # wrapping sum and xor of the little-endian 64-bit words, including an
+    # 8-byte tail and sizes past the kernel's unrolled sweep
+    rng = np.random.default_rng(nbytes)
+    words = rng.integers(0, 1 << 63, size=nbytes // 8, dtype=np.uint64) * np.uint64(3)
+    buf = up(rt, words) if nbytes else rt.alloc(16)
+    out = rt.alloc(16)
+    call("ammon_checksum", rt.handle, None, buf, nbytes, out)
+    s, x = down(out, 2, np.uint64)
+    assert int(s) == int(np.sum(words, dtype=np.uint64))
+    assert int(x) == int(np.bitwise_xor.reduce(words)) if nbytes else int(x) == 0
+    # twice in a row: the result words are cleared by the call itself
+    call("ammon_checksum", rt.handle, None, buf, nbytes, out)
+    np.testing.assert_array_equal(down(out, 2, np.uint64), [s, x])
+    with pytest.raises(AmmonError, match="64-bit words"):
+        call("ammon_checksum", rt.handle, None, buf, 12, out)
+
+
 def test_fill_const(rt):
     buf = rt.alloc(1000 * 4)
     rt.fill(buf, F32, 1000, 2.5)

@@ -1,10 +1,12 @@
 """End-to-end GPU tests of the C++ host layer's model (modules + launch
 sequence + greedy loop) against the oracle: greedy token sequences identical;
 logits and KV caches within 1e-5 relative (normwise) with an fp32 KV cache
-(fp32 or identical bf16 weights); within 2e-2 -- the bf16 bar -- with a bf16
-KV cache, where a last-bit difference in the fp32 K/V before the store can
-flip one bf16 rounding (2^-8 relative); and within 2e-2 of the unrounded
-fp32 model for bf16 weights."""
+(fp32 or identical bf16 weights); within 1e-3 with a bf16 KV cache and the
+same weights on both sides, where the fp32 K/V before the store differ only
+by summation order (~4e-6 relative) and so flip about two bf16 roundings per
+1024-element row, each by one bf16 ulp (at most 2^-7 of the element), which
+moves a row by ~3.5e-4 normwise; and within 2e-2 -- the bf16-weight bar --
+of the unrounded fp32 model for bf16 weights."""
 import json
 import os
 
@@ -18,11 +20,12 @@ from ammon_amd._abi import BF16, F32
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 RTOL = 1e-5
-BF16_TOL = 2e-2
+BF16_KV_TOL = 1e-3  # same weights, bf16 KV cache (rounding flips of new K/V elements)
+BF16_W_TOL = 2e-2   # bf16 weights against the unrounded fp32 model
 
 
 def tol(kv_dtype):
-    return RTOL if kv_dtype == F32 else BF16_TOL
+    return RTOL if kv_dtype == F32 else BF16_KV_TOL
 
 
 def rel_err(got, want):
@@ -116,7 +119,7 @@ def test_gqa_bf16_weights_match_oracle(rt, kv_dtype):
     m.close()
     m = LlamaModel.from_host(rt, cfg, weights)
     for pos, tok in enumerate(prompt):
-        assert rel_err(m.step(tok, pos), m32.step(tok, pos)) <= 2e-2
+        assert rel_err(m.step(tok, pos), m32.step(tok, pos)) <= BF16_W_TOL
     m.close()
 
 

@@ -24,7 +24,11 @@ from ammon_amd._abi import BF16, F32, AmmonError, call
 pytestmark = pytest.mark.gpu
 HERE = os.path.dirname(os.path.abspath(__file__))
 RTOL = 1e-5
-BF16_TOL = 2e-2
+# bf16 KV: the two sides' fp32 K/V differ only by summation order, which can
+# flip a bf16 rounding by one ulp (at most 2^-7 of the element): stored rows
+# within 2^-7 normwise, logits within 1e-3 normwise
+KV_STORE_TOL = 2.0**-7
+BF16_KV_TOL = 1e-3
 
 
 def rel_err(got, want):
@@ -219,7 +223,7 @@ def test_prefill_qkv_rope_store(rt, shape, kv_dtype, use_ws):
     assert rel_err(q.download((T, qd)), want_q) <= RTOL
     got_k = pos_major(kc.download((kv_heads, seq, head), npdt(kv_dtype)), kv_heads, seq, head)
     got_v = pos_major(vc.download((kv_heads, seq, head), npdt(kv_dtype)), kv_heads, seq, head)
-    tol = RTOL if kv_dtype == F32 else BF16_TOL
+    tol = RTOL if kv_dtype == F32 else KV_STORE_TOL
     for got, want in ((got_k, kc_pm), (got_v, vc_pm)):
         assert rel_err(oracle.widen(got, kv_dtype), oracle.widen(want, kv_dtype)) <= tol
         # rows outside [p0, p0 + T) untouched
@@ -321,13 +325,14 @@ def test_model_prefill_matches_stepping(rt, heads, kv_dtype, w_dtype):
         want = stepped.step(tok, pos)
     got = filled.prefill(prompt)
     # fp32 KV: only summation order differs; bf16 KV: a last-bit difference
-    # in an fp32 K/V value can flip its bf16 rounding (2^-8 relative)
-    tol = 1e-4 if kv_dtype == F32 else BF16_TOL
+    # in an fp32 K/V value can flip its bf16 rounding by one ulp
+    tol = 1e-4 if kv_dtype == F32 else BF16_KV_TOL
+    kv_tol = 1e-4 if kv_dtype == F32 else KV_STORE_TOL
     assert rel_err(got, want) <= tol
     for l in range(cfg.n_layers):
         for g, w in zip(filled.kv_layer(l), stepped.kv_layer(l)):
             g, w = oracle.widen(g, kv_dtype), oracle.widen(w, kv_dtype)  # bf16 storage bits
-            assert rel_err(g[: len(prompt)], w[: len(prompt)]) <= tol
+            assert rel_err(g[: len(prompt)], w[: len(prompt)]) <= kv_tol
             np.testing.assert_array_equal(g[len(prompt):], 0)
     # decoding on from the prefilled cache gives the stepped model's tokens
     nxt = oracle.sample_argmax(want)
