@@ -90,9 +90,11 @@ Header read_header(const char *path) {
   c.w_dtype = AMMON_F32;
   c.kv_dtype = AMMON_F32;
   c.use_graph = 1;
-  const uint64_t head = dim / heads, kvd = head * kv;
-  uint64_t floats = (uint64_t)c.vocab * dim + 2ull * L * dim + dim +
-                    (uint64_t)L * (dim * dim + 2 * kvd * dim + dim * dim + 3ull * hidden * dim);
+  // all size arithmetic in 64 bits: dim * dim alone overflows 32 bits for
+  // dim >= 65536
+  const uint64_t D = dim, head = D / heads, kvd = head * kv;
+  uint64_t floats = (uint64_t)c.vocab * D + 2ull * L * D + D +
+                    (uint64_t)L * (D * D + 2 * kvd * D + D * D + 3ull * hidden * D);
   if (hd.format == AMMON_CHECKPOINT_LEGACY) floats += (uint64_t)c.max_seq * head;  // RoPE tables
   if (!hd.shared) floats += (uint64_t)c.vocab * dim;
   hd.expected = hd.data_offset + floats * 4;
@@ -210,12 +212,18 @@ ammon_status ammon_checkpoint_load(ammon_runtime *rt, const char *path, ammon_dt
     const uint32_t head = D / g.n_heads, kvd = head * g.n_kv_heads;
     const bool bf = w_dtype == AMMON_BF16;
     const ammon::DType wt = bf ? ammon::DType::BF16 : ammon::DType::F32;
+    // every tensor is checked against the 32-bit element count of a Shape
+    // before anything is allocated or streamed into it
+    const uint64_t counts[] = {(uint64_t)V * D, (uint64_t)L * D, (uint64_t)L * D * D,
+                               (uint64_t)L * kvd * D, (uint64_t)L * H * D};
+    for (uint64_t n : counts)
+      if (n >= (1ull << 32))
+        throw ammon::Error(AMMON_E_VALIDATION, "checkpoint: a tensor of " + std::to_string(n) +
+                                                   " elements exceeds 2^32 - 1");
     auto make = [&](uint64_t n, ammon::DType dt) -> void * {
       c->bufs.push_back(ammon::Tensor::zeros(c->rt, ammon::Shape::vector((uint32_t)n), dt));
       return c->bufs.back().data();
     };
-    if ((uint64_t)V * D >= (1ull << 32) || (uint64_t)L * H * D >= (1ull << 32))
-      throw ammon::Error(AMMON_E_VALIDATION, "checkpoint: a tensor exceeds 2^32 elements");
     ammon_llama_weights &w = c->w;
     w.tok_emb = make((uint64_t)V * D, wt);
     w.rms_att = (const float *)make((uint64_t)L * D, ammon::DType::F32);

@@ -247,6 +247,14 @@ class LlamaModel : public AutoregressiveModel {
   void ensure_prefill(uint32_t n);
   const float *rope_table();
   void deposit(uint32_t token, uint32_t pos, ammon_stream stream);
+  // After `stream` has drained (it waits for it): throws if a one-launch
+  // block or the persistent kernel flagged a grid barrier that stopped
+  // waiting (that launch's results are invalid).
+  void check_blocks(ammon_stream stream) const {
+    if (persistent_) persistent_->check(stream);
+    attn_.check(stream);
+    ffn_.check(stream);
+  }
 
   Runtime rt_;
   ammon_llama_config c_;
@@ -285,6 +293,7 @@ AttentionOptions attention_options(const ammon_llama_config &c) {
   o.theta = c.theta;
   o.eps = c.eps;
   o.split_len = c.split_len;
+  o.one_launch = c.one_launch_blocks != 0;
   return o;
 }
 
@@ -306,7 +315,7 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
       kv_dim_(head_ * c.n_kv_heads),
       embed_(rt),
       attn_(rt, c.dim, c.n_heads, c.max_seq, attention_options(c)),
-      ffn_(rt, c.dim, c.hidden, c.eps),
+      ffn_(rt, c.dim, c.hidden, c.eps, c.one_launch_blocks != 0),
       lm_head_(rt),
       cache_(rt, c.n_layers, c.max_seq, c.n_kv_heads, head_, dt(c.kv_dtype)) {
   const DType wd = dt(c.w_dtype);
@@ -409,7 +418,7 @@ const std::vector<float> &LlamaModel::step(uint32_t token, uint32_t pos) {
                      AMMON_COPY_D2H, stream_),
         "logits");
   check(ammon_stream_synchronize(rt_.raw(), stream_), "step");
-  if (persistent_) persistent_->check(stream_);
+  check_blocks(stream_);
   std::memcpy(host_logits_.data(), pinned_logits_, sizeof(float) * c_.vocab);
   return host_logits_;
 }
@@ -442,7 +451,7 @@ GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prom
   }
   check(ammon_event_record(rt_.raw(), e1, st), "event");
   check(ammon_stream_synchronize(rt_.raw(), st), "generate");
-  if (persistent_) persistent_->check(st);
+  check_blocks(st);
   float ms = 0.f;
   if (steps > 1) check(ammon_event_elapsed_ms(rt_.raw(), e0, e1, &ms), "event");
   ammon_event_destroy(rt_.raw(), e0);
@@ -485,7 +494,7 @@ void LlamaModel::decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, in
                        sizeof(int32_t) * n_steps, AMMON_COPY_D2H, stream_),
           "tokens");
     check(ammon_stream_synchronize(rt_.raw(), stream_), "decode");
-    if (persistent_) persistent_->check(stream_);
+    check_blocks(stream_);
   }
 }
 
@@ -630,7 +639,7 @@ GenerateTokenOutput LlamaModel::generate_prefill(const std::vector<int32_t> &pro
   }
   check(ammon_event_record(rt, e1, st), "event");
   check(ammon_stream_synchronize(rt, st), "generate");
-  if (persistent_) persistent_->check(st);
+  check_blocks(st);
   float ms = 0.f;
   const uint32_t decoded = steps - n_prompt;
   if (decoded > 0) check(ammon_event_elapsed_ms(rt, e0, e1, &ms), "event");
@@ -659,7 +668,7 @@ void LlamaModel::read_tokens(uint32_t start, uint32_t n, int32_t *out) {
   if ((uint64_t)start + n > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "tokens: range exceeds max_seq");
   check(ammon_stream_synchronize(rt_.raw(), stream_), "tokens");
-  if (persistent_) persistent_->check(stream_);
+  check_blocks(stream_);
   if (!n) return;
   check(ammon_memcpy(rt_.raw(), out, (int32_t *)tokens_.data() + start, sizeof(int32_t) * n,
                      AMMON_COPY_D2H, stream_),

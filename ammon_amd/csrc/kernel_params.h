@@ -71,6 +71,9 @@ typedef struct {
   float *out;               /* [q_heads, head] (combine) */
   uint32_t q_heads, kv_heads, head, seq, split_len, splits;
   uint32_t pos_add;         /* added to step->position */
+  uint32_t limit;           /* positions at or past it (<= seq) are out of range:
+                               NaN output, no partial (seq for decode; the
+                               positions the grid and scratch cover for prefill) */
 } ammon_k_attention;
 
 typedef struct {
@@ -156,6 +159,27 @@ typedef struct {
   uint32_t dtype;
   uint32_t bits; /* fill: raw 32-bit pattern (f32) or 16-bit (bf16) */
 } ammon_k_fill;
+
+/* Fused blocks: one launch per attention block (norm + QKV + RoPE + K/V
+ * store, split-K attention, merge, output projection + residual) or SwiGLU
+ * block (norm + gate/up + SwiGLU, down projection + residual), the phases
+ * separated by grid barriers over `sync` (AMMON_TOKEN_SYNC_WORDS words,
+ * zero before a launch and left zero by every launch that completes; the
+ * error word is set if a barrier wait gave up). */
+typedef struct {
+  ammon_k_gemv qkv;         /* mode QKV: y = q, caches at step->position */
+  ammon_k_gemv wo;          /* mode RESIDUAL: x += Wo att */
+  ammon_k_attention att;    /* q, caches, partial, out = att */
+  uint32_t *sync;
+  uint32_t spin_limit;
+} ammon_k_attn_block;
+
+typedef struct {
+  ammon_k_gemv gate_up;     /* mode SWIGLU: y = hb */
+  ammon_k_gemv down;        /* mode RESIDUAL: x += W2 hb */
+  uint32_t *sync;
+  uint32_t spin_limit;
+} ammon_k_ffn_block;
 
 /* Persistent decode-token kernel: one cooperative launch runs a whole decode
  * token (embed, every layer, final norm + LM head, optionally the greedy

@@ -115,7 +115,7 @@ struct AttnPartial {
     split = split_;
     g = g_;
     pos = p.step->position + p.pos_add;
-    if (pos >= p.seq) return false;
+    if (pos >= p.limit) return false;
     t0 = split * p.split_len;
     if (t0 > pos) return false;  // dead split: writes nothing
     n = min(p.split_len, pos + 1 - t0);
@@ -323,26 +323,32 @@ struct AttnPartialMfma {
 
   // Positions past the split read zero without touching memory, so loads
   // are issued unconditionally and the wait counts stay exact.
-  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) const {
+  // Rows at or past `rows` (of the split) read as zero.
+  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4], uint32_t rows) const {
     const uint32_t tk = c0 + 16 * wave + (lane & 15);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const uint32_t off = tk < n ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+      const uint32_t off = tk < rows ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
       kr[kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, AMMON_HANDOFF_CPOL);
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t tv = c0 + 16 * wave + 4 * k + (lane >> 4);
-      const uint32_t off = tv < n ? (tv * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
+      const uint32_t off = tv < rows ? (tv * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
       vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, AMMON_HANDOFF_CPOL);
     }
   }
+  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) const {
+    load_chunk(c0, kr, vr, n);
+  }
 
-  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
+  // The unit's split and cache resources; false for a dead split (start past
+  // the position) or an out-of-range position, which write nothing.
+  AMMON_DEV bool setup(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
     split = split_;
     g = g_;
     pos = p.step->position + p.pos_add;
-    if (pos >= p.seq) return false;
+    if (pos >= p.limit) return false;
     t0 = split * p.split_len;
     if (t0 > pos) return false;  // dead split: writes nothing
     n = min(p.split_len, pos + 1 - t0);
@@ -350,21 +356,51 @@ struct AttnPartialMfma {
     wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     kres = make_rsrc((const uint16_t *)p.k_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
     vres = make_rsrc((const uint16_t *)p.v_cache + ((size_t)g * p.seq + t0) * HEAD, n * HEAD * 2);
+    return true;
+  }
+
+  AMMON_DEV void load_q(const ammon_k_attention &p) {
+    const uint32_t h = lane & 15;
+    const bool ok = h < GMAX;
+    const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      qraw[kk][0] = ok ? ld_in4(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qraw[kk][1] = ok ? ld_in4(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+  }
+
+  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
+    if (!setup(p, split_, g_)) return false;
     // q first: loads complete in order, so the first chunk's MFMAs then wait
     // only for q and that chunk, not for the later chunk's K/V as well
-    {
-      const uint32_t h = lane & 15;
-      const bool ok = h < GMAX;
-      const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        qraw[kk][0] = ok ? ld_in4(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-        qraw[kk][1] = ok ? ld_in4(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-      }
-    }
+    load_q(p);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b]);
     return true;
+  }
+
+  // begin() in two steps, for a caller whose q and newest K/V row are stored
+  // by other workgroups of the same launch: prefetch() -- before they are --
+  // requests the first NBUF chunks with every row except the position's
+  // (which may not exist yet); finish() -- once they are -- requests q and,
+  // if the position's row lies in a prefetched chunk, that chunk again in
+  // full.  run() then sees exactly what begin() would have loaded.
+  AMMON_DEV bool prefetch(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
+    if (!setup(p, split_, g_)) return false;
+    const uint32_t before = t0 + n - 1 == pos ? n - 1 : n;  // rows older than the position
+#pragma unroll
+    for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b], before);
+    return true;
+  }
+  AMMON_DEV void finish(const ammon_k_attention &p) {
+    load_q(p);
+    if (t0 + n - 1 == pos) {
+      const uint32_t cb = (pos - t0) / CHUNK;  // chunk of the position's row
+#pragma unroll
+      for (int b = 0; b < NBUF; ++b)
+        if ((uint32_t)b == cb) load_chunk(b * CHUNK, kb[b], vb[b]);
+    }
   }
 
   // lds: att_lds_floats(GMAX, 8) floats.
@@ -535,9 +571,9 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
 //   total = ((0 + a_0) + a_1) + ... + a_63,  L likewise;  out[d] = total / L
 // (lanes without a live split add +0).  Two layouts compute exactly this:
 //
-// Units (q head, head / 32 dim slices) of a workgroup: lane (split lane sl,
-// dim quarter) covers splits sl, sl + 64, ...; with up to COMB_ROUNDS * 64
-// live splits it loads each split's max, sum and 8 of the slice's dims in
+// Units (q head, head / 32 or head / 8 dim slices) of a workgroup: lane
+// (split lane sl, dim quarter) covers splits sl, sl + 64, ...; with up to
+// COMB_ROUNDS * 64 live splits it loads each split's max, sum and its dims in
 // one round trip and keeps them in registers while the workgroup max M
 // forms (more splits take a second pass over the buffer); the split lanes
 // are summed through LDS.  Every workgroup of a head computes the same M.
@@ -549,34 +585,42 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
 // mostly idle lanes.
 #define COMB_SPLIT_LANES 64
 #define COMB_ROUNDS 4
-// LDS floats of one combine unit: per split lane 32 dims + 1 pad, its sum,
-// and the block reduction slots.
-#define COMB_LDS_FLOATS (COMB_SPLIT_LANES * 33 + COMB_SPLIT_LANES + AMMON_WAVES)
+// LDS floats of one combine unit over SLICE dims: per split lane the slice
+// + 1 pad, its sum, and the block reduction slots.
+#define COMB_LDS_FLOATS_W(SLICE) (COMB_SPLIT_LANES * ((SLICE) + 1) + COMB_SPLIT_LANES + AMMON_WAVES)
+#define COMB_LDS_FLOATS COMB_LDS_FLOATS_W(32)
 
-// Unit (q head h, 32-dim slice) of pass 2; lds holds COMB_LDS_FLOATS floats.
+// Unit (q head h, SLICE-dim slice) of pass 2 (SLICE 32 or 8: each lane
+// owns SLICE / 4 dims of one split lane; the per-dim arithmetic does not
+// depend on SLICE); lds holds COMB_LDS_FLOATS_W(SLICE) floats.
+template <int SLICE = 32>
 AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, uint32_t slice,
                                       float *lds) {
-  float(*s_acc)[33] = (float(*)[33])lds;
-  float *s_l = lds + COMB_SPLIT_LANES * 33;
+  static_assert(SLICE == 32 || SLICE == 8, "slice width");
+  constexpr int DQ = SLICE / 4;  // dims per lane
+  float(*s_acc)[SLICE + 1] = (float(*)[SLICE + 1])lds;
+  float *s_l = lds + COMB_SPLIT_LANES * (SLICE + 1);
   float *red = s_l + COMB_SPLIT_LANES;
   const uint32_t head = p.head, slot = head + 2;
-  const uint32_t d0 = slice * 32;
+  const uint32_t d0 = slice * SLICE;
   float *out = p.out + (size_t)h * head;
   const uint32_t pos = p.step->position + p.pos_add;
-  if (pos >= p.seq) {
-    if (threadIdx.x < 32 && d0 + threadIdx.x < head)
+  if (pos >= p.limit) {
+    if (threadIdx.x < SLICE && d0 + threadIdx.x < head)
       st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));
     return;
   }
   const uint32_t live = min(pos / p.split_len + 1, p.splits);
   const float *base = p.partial + (size_t)h * p.splits * slot;
-  const uint32_t sl = threadIdx.x >> 2;        // split lane, 0..63
-  const uint32_t dq = (threadIdx.x & 3) * 8;   // 8 dims of the slice
+  const uint32_t sl = threadIdx.x >> 2;         // split lane, 0..63
+  const uint32_t dq = (threadIdx.x & 3) * DQ;  // DQ dims of the slice
 
-  float a[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float a[DQ];
+#pragma unroll
+  for (int k = 0; k < DQ; ++k) a[k] = 0.f;
   float l = 0.f;
   if (live <= COMB_ROUNDS * COMB_SPLIT_LANES) {
-    float mv[COMB_ROUNDS], lv[COMB_ROUNDS], dv[COMB_ROUNDS][8];
+    float mv[COMB_ROUNDS], lv[COMB_ROUNDS], dv[COMB_ROUNDS][DQ];
 #pragma unroll
     for (int r = 0; r < COMB_ROUNDS; ++r) {
       const uint32_t s = sl + r * COMB_SPLIT_LANES;
@@ -584,7 +628,7 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
       mv[r] = s < live ? ld_in(row + head) : -INFINITY;
       lv[r] = ld_in(row + head + 1);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < DQ; ++k) {
         const uint32_t d = d0 + dq + k;
         dv[r][k] = d < head ? ld_in(row + d) : 0.f;
       }
@@ -599,7 +643,7 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
       const float w = expf(mv[r] - M);
       if ((threadIdx.x & 3) == 0) l = fmaf(lv[r], w, l);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) a[k] = fmaf(dv[r][k], w, a[k]);
+      for (int k = 0; k < DQ; ++k) a[k] = fmaf(dv[r][k], w, a[k]);
     }
   } else {
     float m = -INFINITY;
@@ -611,17 +655,17 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
       const float w = expf(ld_in(row + head) - M);
       if ((threadIdx.x & 3) == 0) l = fmaf(ld_in(row + head + 1), w, l);
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
+      for (int k = 0; k < DQ; ++k) {
         const uint32_t d = d0 + dq + k;
         if (d < head) a[k] = fmaf(ld_in(row + d), w, a[k]);
       }
     }
   }
 #pragma unroll
-  for (int k = 0; k < 8; ++k) s_acc[sl][dq + k] = a[k];
+  for (int k = 0; k < DQ; ++k) s_acc[sl][dq + k] = a[k];
   if ((threadIdx.x & 3) == 0) s_l[sl] = l;
   __syncthreads();
-  if (threadIdx.x < 32) {
+  if (threadIdx.x < SLICE) {
     float total = 0.f, L = 0.f;
     for (uint32_t s = 0; s < COMB_SPLIT_LANES; ++s) {
       total += s_acc[s][threadIdx.x];
@@ -640,7 +684,7 @@ AMMON_DEV void attention_combine_wave(const ammon_k_attention &p, uint32_t h) {
   const bool mine = 2 * lane < head;
   float *out = p.out + (size_t)h * head + 2 * lane;
   const uint32_t pos = p.step->position + p.pos_add;
-  if (pos >= p.seq) {
+  if (pos >= p.limit) {
     if (mine) {
       st_out(out, __uint_as_float(0x7fc00000u));
       st_out(out + 1, __uint_as_float(0x7fc00000u));

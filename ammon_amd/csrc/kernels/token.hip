@@ -31,18 +31,11 @@
 // (weights, norm weights, the RoPE table) and the DecodeStep (written by the
 // previous launch) use plain loads.
 //
-// Barrier: every wave waits for its stores to complete, thread 0 counts the
-// workgroup in one of 8 group counters (blockIdx % 8), the last arrival of
-// a group bumps the top counter; waiters poll the top counter.  Counters
-// only grow within a launch; workgroup 0 zeroes them after the final
-// barrier, when every other workgroup has arrived for the last time.  A
-// bounded poll marks sync[AMMON_TOKEN_SYNC_ERR] and lets the kernel run to
-// its end instead of hanging (results are then invalid; the host reports
-// it).
-//
-// With a trace buffer, thread 0 of every workgroup stamps the device clock
-// when it arrives at and when it leaves each barrier (phase timing and load
-// balance without a profiler; the stamps are a few stores per barrier).
+// Barrier: GridSync (grid_sync.h), hierarchical counters with bounded
+// polls.  Workgroup 0 waits at the final barrier (the greedy step needs
+// every candidate) and then zeroes the counters for the next launch.  With a
+// trace buffer every workgroup stamps the device clock at each barrier
+// (phase timing and load balance without a profiler).
 //
 // Requires all gridDim.x workgroups to be co-resident (cooperative launch).
 // results cross workgroups within the launch: agent-scope stores and loads
@@ -50,62 +43,9 @@
 #include "argmax_impl.h"
 #include "attention_impl.h"
 #include "gemv_impl.h"
+#include "grid_sync.h"
 
 namespace {
-
-struct GridSync {
-  uint32_t *sync;
-  uint32_t nwg;
-  uint32_t k;  // barriers passed by this workgroup
-  uint32_t spin_limit;
-  uint64_t *trace;
-  uint32_t trace_slots;
-
-  AMMON_DEV void stamp(uint32_t half) const {
-    if (trace && k - 1 < trace_slots)
-      trace[(size_t)(2 * (k - 1) + half) * nwg + blockIdx.x] = __builtin_amdgcn_s_memrealtime();
-  }
-
-  AMMON_DEV uint32_t poll(const uint32_t *a) const {
-    return __hip_atomic_load(a, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-
-  // Count this workgroup in once its stores have completed.
-  AMMON_DEV void arrive() {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are at the coherence point
-    __syncthreads();
-    ++k;
-    if (threadIdx.x == 0) {
-      const uint32_t grp = blockIdx.x & 7u;
-      const uint32_t per = (nwg - grp + 7u) / 8u;  // workgroups in this group
-      const uint32_t old =
-          __hip_atomic_fetch_add(sync + 64 * (1 + grp), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      if (old + 1 == per * k)
-        __hip_atomic_fetch_add(sync, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      stamp(0);
-    }
-  }
-
-  // Wait until every workgroup has arrived k times.
-  AMMON_DEV void wait() {
-    if (threadIdx.x == 0) {
-      const uint32_t target = 8u * k;
-      uint32_t it = 0;
-      if (poll(sync + AMMON_TOKEN_SYNC_ERR) == 0) {
-        while (poll(sync) < target) {
-          if (++it > spin_limit) {
-            __hip_atomic_store(sync + AMMON_TOKEN_SYNC_ERR, 1u, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-            break;
-          }
-          __builtin_amdgcn_s_sleep(1);
-        }
-      }
-      stamp(1);
-    }
-    __syncthreads();
-  }
-};
 
 template <typename KV>
 AMMON_DEV size_t kv_layer_elems(const ammon_k_token &P) {
@@ -201,6 +141,7 @@ AMMON_DEV void decode_token(const ammon_k_token &P) {
     a.kv_heads = P.kv_heads;
     a.head = head;
     a.seq = P.seq;
+    a.limit = P.seq;
     a.split_len = P.split_len;
     a.splits = P.splits;
     {

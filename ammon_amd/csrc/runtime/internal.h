@@ -41,6 +41,9 @@ struct Kernels {
   hipFunction_t fill_normal = nullptr;
   hipFunction_t fill_const = nullptr;
   hipFunction_t checksum = nullptr;
+  // one-launch blocks (bf16): attention [G index 1, 2, 4], SwiGLU
+  hipFunction_t attn_block[kAttGroups] = {};
+  hipFunction_t ffn_block = nullptr;
   // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
   hipFunction_t token[2][kAttGroups] = {};
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]

@@ -15,6 +15,10 @@
 
 using namespace ammon_rt;
 
+static_assert(AMMON_BLOCK_SYNC_WORDS == AMMON_TOKEN_SYNC_WORDS &&
+                  AMMON_BLOCK_SYNC_ERR == AMMON_TOKEN_SYNC_ERR,
+              "block barrier words: one layout for the header and the kernels");
+
 namespace {
 
 using DeviceGuard = ammon_rt::DeviceScope;
@@ -79,10 +83,11 @@ struct GemvArgs {
   uint32_t cand_cap;
 };
 
-// Validates, packs and launches a GEMV; *grid_out (optional) receives the
-// workgroup count (PLAIN_ARGMAX writes one candidate per workgroup).
-ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemvArgs &a,
-                                   const char *what, uint32_t *grid_out = nullptr) {
+// Validates and packs a GEMV: *p receives the kernel parameters, *lds_out
+// the bytes of LDS its x staging needs, *vec_out whether the 16-byte-chunk
+// (vector) kernels apply.
+ammon_status gemv_pack(ammon_runtime *rt, const GemvArgs &a, const char *what, ammon_k_gemv *out,
+                       size_t *lds_out, int *vec_out) {
   AMMON_CHECK(valid_dtype(a.w_dtype), "%s: unknown weight dtype %d", what, (int)a.w_dtype);
   AMMON_CHECK(a.w0 && a.x && a.y, "%s: NULL weight, x or y", what);
   AMMON_CHECK(a.n > 0 && a.d > 0, "%s: empty matrix (d=%u, n=%u)", what, a.d, a.n);
@@ -104,10 +109,9 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   AMMON_CHECK(!overlaps(a.x, (size_t)a.n * 4, a.y, ybytes), "%s: y overlaps x", what);
   if (a.residual)
     AMMON_CHECK(!overlaps(a.x, (size_t)a.n * 4, a.residual, ybytes), "%s: residual overlaps x", what);
-  if (stream == AMMON_STREAM_VALIDATE) return AMMON_OK;
 
-
-  ammon_k_gemv p = {};
+  ammon_k_gemv &p = *out;
+  p = ammon_k_gemv{};
   p.w0 = a.w0;
   p.w1 = a.w1;
   p.w2 = a.w2;
@@ -132,9 +136,21 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   p.kv_dtype = (uint32_t)a.kv_dtype;
   p.cand_v = a.cand_v;
   p.cand_i = a.cand_i;
+  *lds_out = shmem;
+  *vec_out = vec_ok;
+  return AMMON_OK;
+}
 
-  const int dt = bf ? 1 : 0;
-  const int vec = vec_ok;
+// Validates, packs and launches a GEMV; *grid_out (optional) receives the
+// workgroup count (PLAIN_ARGMAX writes one candidate per workgroup).
+ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemvArgs &a,
+                                   const char *what, uint32_t *grid_out = nullptr) {
+  ammon_k_gemv p;
+  size_t shmem = 0;
+  int vec = 0;
+  const ammon_status status = gemv_pack(rt, a, what, &p, &shmem, &vec);
+  if (status != AMMON_OK || stream == AMMON_STREAM_VALIDATE) return status;
+  const int dt = a.w_dtype == AMMON_BF16 ? 1 : 0;
   size_t lds = shmem;
   // PLAIN_ARGMAX reduces the workgroup's candidates in x's LDS
   if (a.mode == AMMON_GEMV_PLAIN_ARGMAX) lds = std::max<size_t>(lds, 2 * kWorkgroup * 4);
@@ -354,7 +370,7 @@ ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, con
   VALIDATE_ONLY();
   const uint32_t splits = ammon_attention_splits(seq, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, nullptr,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0};
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, seq};
   return launch(rt, stream, f, splits, kv_heads, 0, p, "attention_partial");
 }
 
@@ -377,7 +393,7 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
-                         ammon_attention_splits(seq, split_len), 0};
+                         ammon_attention_splits(seq, split_len), 0, seq};
   return launch(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), 0, p,
                 "attention_combine");
 }
@@ -436,10 +452,12 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
   hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache);
   AMMON_CHECK(f, "attention_prefill: head %u needs an even width above 64", head);
   VALIDATE_ONLY();
-  // the partial layout and the grid cover ctx positions: [tokens][q_heads][splits][head + 2]
+  // the partial layout and the grid cover ctx positions: [tokens][q_heads][splits][head + 2];
+  // a token at position >= ctx (the host cannot see step->position) gets the
+  // out-of-range treatment -- NaN output, no partial -- like one past seq
   const uint32_t splits = ammon_attention_splits(ctx, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, out,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0};
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx};
   st = launch3(rt, stream, f, splits, kv_heads, tokens, 0, p, "attention_prefill");
   if (st != AMMON_OK) return st;
   return launch3(rt, stream, rt->k.att_combine_waves, cdiv(q_heads, kWaves), 1, tokens, 0, p,
@@ -860,6 +878,211 @@ ammon_status ammon_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const 
   a.eps = eps;
   a.y = hb;
   return gemv_check_and_launch(rt, stream, a, "gate_up_swiglu");
+}
+
+// ---- one-launch blocks --------------------------------------------------------------------
+// A barrier wait gives up after this many polls (each sleeps ~64 clocks
+// and waits for a load: well over 0.1 s) and flags the launch.
+static uint32_t block_spin_limit() {
+  uint32_t limit = 200000;
+  if (const char *env = std::getenv("AMMON_BLOCK_SPIN_LIMIT")) {
+    const long v = std::atol(env);
+    if (v > 0) limit = (uint32_t)std::min<long>(v, 200000);
+  }
+  return limit;
+}
+
+static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// Resident workgroups for a barrier kernel: two per CU where the occupancy
+// allows (the grid every phase is tuned for), else one.
+static uint32_t block_grid(ammon_runtime *rt, hipFunction_t f, size_t lds) {
+  const uint32_t occ = occupancy(rt, f, lds);
+  return (uint32_t)std::max(rt->info.compute_units, 1) * std::min<uint32_t>(occ, 2);
+}
+
+ammon_status ammon_attention_block(ammon_runtime *rt, ammon_stream stream, float *x,
+                                   const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                   const void *wq, const void *wk, const void *wv, const void *wo,
+                                   ammon_dtype w_dtype, uint32_t dim, uint32_t q_heads,
+                                   uint32_t kv_heads, uint32_t head, void *k_cache, void *v_cache,
+                                   ammon_dtype kv_dtype, uint32_t seq,
+                                   const ammon_decode_step *step, const float *table,
+                                   uint32_t split_len, float *q, float *att, float *partial,
+                                   size_t partial_bytes, uint32_t *sync) {
+  REQUIRE_RT();
+  const char *what = "attention_block";
+  AMMON_CHECK(x && wo && q && att && partial && sync, "%s: NULL x, wo, q, att, partial or sync",
+              what);
+  AMMON_CHECK(w_dtype == AMMON_BF16 && kv_dtype == AMMON_BF16,
+              "%s: one launch needs bf16 weights and a bf16 KV cache", what);
+  AMMON_CHECK(head == 128, "%s: one launch needs head 128, got %u", what, head);
+  const uint32_t g = kv_heads ? q_heads / kv_heads : 0;
+  AMMON_CHECK(kv_heads > 0 && q_heads % kv_heads == 0 && (g == 1 || g == 2 || g == 4),
+              "%s: one launch needs 1, 2 or 4 q heads per kv head", what);
+  AMMON_CHECK(dim % 8 == 0 && aligned16(wq) && aligned16(wk) && aligned16(wv) && aligned16(wo) &&
+                  aligned16(x) && aligned16(q) && aligned16(att),
+              "%s: x, q, att and the weights must be 16-byte aligned with dim a multiple of 8",
+              what);
+  // the launch list's contract, with its own messages
+  ammon_status st =
+      ammon_qkv_rope_store(rt, AMMON_STREAM_VALIDATE, x, norm_weight, norm_dtype, eps, wq, wk, wv,
+                           w_dtype, dim, q_heads, kv_heads, head, q, k_cache, v_cache, kv_dtype,
+                           seq, step, table);
+  if (st != AMMON_OK) return st;
+  st = ammon_attention_decode(rt, AMMON_STREAM_VALIDATE, q, q_heads, k_cache, v_cache, kv_dtype,
+                              kv_heads, head, seq, step, split_len, partial, partial_bytes, att);
+  if (st != AMMON_OK) return st;
+  const uint32_t q_dim = q_heads * head, kv_dim = kv_heads * head;
+  st = ammon_gemv(rt, AMMON_STREAM_VALIDATE, wo, w_dtype, dim, q_dim, att, x, x);
+  if (st != AMMON_OK) return st;
+  const size_t qb = (size_t)q_dim * 4, pb = partial_bytes, sb = AMMON_BLOCK_SYNC_WORDS * 4;
+  AMMON_CHECK(!overlaps(q, qb, att, qb) && !overlaps(partial, pb, q, qb) &&
+                  !overlaps(partial, pb, att, qb) && !overlaps(sync, sb, q, qb) &&
+                  !overlaps(sync, sb, att, qb) && !overlaps(sync, sb, partial, pb) &&
+                  !overlaps(sync, sb, x, (size_t)dim * 4),
+              "%s: q, att, partial and sync must not overlap each other or x", what);
+
+  ammon_k_attn_block p = {};
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_QKV;
+  a.w0 = wq;
+  a.w1 = wk;
+  a.w2 = wv;
+  a.w_dtype = w_dtype;
+  a.d = q_dim;
+  a.n = dim;
+  a.rows = q_dim + 2 * kv_dim;
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = q;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  a.step = step;
+  a.table = table;
+  a.kv_dim = kv_dim;
+  a.head = head;
+  a.seq = seq;
+  a.kv_dtype = kv_dtype;
+  size_t lds_qkv = 0, lds_wo = 0;
+  int vec_qkv = 0, vec_wo = 0;
+  st = gemv_pack(rt, a, what, &p.qkv, &lds_qkv, &vec_qkv);
+  if (st != AMMON_OK) return st;
+  GemvArgs b = {};
+  b.mode = AMMON_GEMV_RESIDUAL;
+  b.w0 = wo;
+  b.w_dtype = w_dtype;
+  b.d = dim;
+  b.n = q_dim;
+  b.rows = dim;
+  b.x = att;
+  b.residual = x;
+  b.y = x;
+  st = gemv_pack(rt, b, what, &p.wo, &lds_wo, &vec_wo);
+  if (st != AMMON_OK) return st;
+  AMMON_CHECK(vec_qkv && vec_wo, "%s: rows must be whole 16-byte chunks", what);
+  const uint32_t splits = ammon_attention_splits(seq, split_len);
+  p.att = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, att,
+           q_heads, kv_heads, head, seq, split_len, splits, 0, seq};
+  p.sync = sync;
+  p.spin_limit = block_spin_limit();
+  VALIDATE_ONLY();
+  hipFunction_t fn = rt->k.attn_block[att_group_index(g)];
+  AMMON_CHECK(fn != nullptr, "%s: kernel not loaded", what);
+  // LDS: x staged for either GEMV, a split-K unit's merge, or a merge unit
+  const size_t att_lds = ((size_t)kWorkgroup * (g * 8 + 1) + (size_t)kWorkgroup * g) * 4;
+  const size_t comb_lds = (64 * 9 + 64 + kWaves) * 4;
+  const size_t lds = std::max(std::max(lds_qkv, lds_wo), std::max(att_lds, comb_lds));
+  const uint32_t grid = block_grid(rt, fn, lds);
+  AMMON_CHECK(grid >= 8, "%s: %u resident workgroups are too few for the grid barrier", what,
+              grid);
+  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
+}
+
+ammon_status ammon_swiglu_block(ammon_runtime *rt, ammon_stream stream, float *x,
+                                const void *norm_weight, ammon_dtype norm_dtype, float eps,
+                                const void *w1, const void *w3, const void *w2,
+                                ammon_dtype w_dtype, uint32_t dim, uint32_t hidden, float *hb,
+                                uint32_t *sync) {
+  REQUIRE_RT();
+  const char *what = "swiglu_block";
+  AMMON_CHECK(x && w2 && hb && sync, "%s: NULL x, w2, hb or sync", what);
+  AMMON_CHECK(w_dtype == AMMON_BF16, "%s: one launch needs bf16 weights", what);
+  AMMON_CHECK(dim % 8 == 0 && hidden % 8 == 0 && aligned16(w1) && aligned16(w3) &&
+                  aligned16(w2) && aligned16(x) && aligned16(hb),
+              "%s: x, hb and the weights must be 16-byte aligned with dim and hidden multiples "
+              "of 8",
+              what);
+  ammon_status st = ammon_gate_up_swiglu(rt, AMMON_STREAM_VALIDATE, x, norm_weight, norm_dtype,
+                                         eps, w1, w3, w_dtype, dim, hidden, hb);
+  if (st != AMMON_OK) return st;
+  st = ammon_gemv(rt, AMMON_STREAM_VALIDATE, w2, w_dtype, dim, hidden, hb, x, x);
+  if (st != AMMON_OK) return st;
+  const size_t sb = AMMON_BLOCK_SYNC_WORDS * 4;
+  AMMON_CHECK(!overlaps(sync, sb, hb, (size_t)hidden * 4) &&
+                  !overlaps(sync, sb, x, (size_t)dim * 4),
+              "%s: sync must not overlap x or hb", what);
+
+  ammon_k_ffn_block p = {};
+  GemvArgs a = {};
+  a.mode = AMMON_GEMV_SWIGLU;
+  a.w0 = w1;
+  a.w1 = w3;
+  a.w_dtype = w_dtype;
+  a.d = hidden;
+  a.n = dim;
+  a.rows = 2 * hidden;
+  a.x = x;
+  a.norm_w = norm_weight;
+  a.norm_dtype = norm_dtype;
+  a.eps = eps;
+  a.y = hb;
+  size_t lds_gu = 0, lds_down = 0;
+  int vec_gu = 0, vec_down = 0;
+  st = gemv_pack(rt, a, what, &p.gate_up, &lds_gu, &vec_gu);
+  if (st != AMMON_OK) return st;
+  GemvArgs b = {};
+  b.mode = AMMON_GEMV_RESIDUAL;
+  b.w0 = w2;
+  b.w_dtype = w_dtype;
+  b.d = dim;
+  b.n = hidden;
+  b.rows = dim;
+  b.x = hb;
+  b.residual = x;
+  b.y = x;
+  st = gemv_pack(rt, b, what, &p.down, &lds_down, &vec_down);
+  if (st != AMMON_OK) return st;
+  AMMON_CHECK(vec_gu && vec_down, "%s: rows must be whole 16-byte chunks", what);
+  p.sync = sync;
+  p.spin_limit = block_spin_limit();
+  VALIDATE_ONLY();
+  hipFunction_t fn = rt->k.ffn_block;
+  AMMON_CHECK(fn != nullptr, "%s: kernel not loaded", what);
+  const size_t lds = std::max(lds_gu, lds_down);
+  const uint32_t grid = block_grid(rt, fn, lds);
+  AMMON_CHECK(grid >= 8, "%s: %u resident workgroups are too few for the grid barrier", what,
+              grid);
+  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
+}
+
+ammon_status ammon_block_sync_check(ammon_runtime *rt, ammon_stream stream, uint32_t *sync) {
+  REQUIRE_RT();
+  AMMON_CHECK(sync != nullptr, "block_sync_check: NULL sync");
+  uint32_t err = 0;
+  ammon_status st = ammon_memcpy(rt, &err, sync + AMMON_BLOCK_SYNC_ERR, sizeof err,
+                                 AMMON_COPY_D2H, stream);
+  if (st == AMMON_OK) st = ammon_stream_synchronize(rt, stream);
+  if (st != AMMON_OK || err == 0) return st;
+  // the launch's results are invalid; clear the words for the next one
+  st = ammon_fill(rt, stream, sync, AMMON_F32, AMMON_BLOCK_SYNC_WORDS, 0.f);
+  if (st == AMMON_OK) st = ammon_stream_synchronize(rt, stream);
+  if (st != AMMON_OK) return st;
+  return set_error(AMMON_E_HIP,
+                   "a grid barrier of a one-launch block timed out (workgroups not co-resident); "
+                   "the results of that launch are invalid");
 }
 
 // ---- argmax ---------------------------------------------------------------------------------

@@ -28,6 +28,7 @@ AMMON_BLOB(gemv)
 AMMON_BLOB(misc)
 AMMON_BLOB(token)
 AMMON_BLOB(prefill)
+AMMON_BLOB(block)
 
 namespace ammon_rt {
 
@@ -80,7 +81,8 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   } blobs[] = {{"embed", ammon_co_embed}, {"norm", ammon_co_norm},
                {"rope", ammon_co_rope},   {"attention", ammon_co_attention},
                {"gemv", ammon_co_gemv},   {"misc", ammon_co_misc},
-               {"token", ammon_co_token}, {"prefill", ammon_co_prefill}};
+               {"token", ammon_co_token}, {"prefill", ammon_co_prefill},
+               {"block", ammon_co_block}};
   constexpr int kModules = (int)(sizeof(blobs) / sizeof(blobs[0]));
   hipModule_t mods[kModules];
   for (int i = 0; i < kModules; ++i) {
@@ -156,6 +158,12 @@ static ammon_status load_kernels(ammon_runtime *rt) {
         }
   R(7, "ammon_gemm_reduce", k.gemm_reduce);
   R(7, "ammon_gemm_reduce_qkv", k.gemm_reduce_qkv);
+  for (int g = 0; g < 3; ++g) {
+    char name[96];
+    snprintf(name, sizeof name, "ammon_attn_block_bf16_g%d", gs[g]);
+    R(8, name, k.attn_block[g]);
+  }
+  R(8, "ammon_ffn_block_bf16", k.ffn_block);
   for (int t = 0; t < 2; ++t)
     for (int r = 0; r < 2; ++r)
       for (int m = 0; m < kGemvModes; ++m) {

@@ -95,13 +95,15 @@ class LlamaModel:
     """
 
     def __init__(self, rt: Runtime, cfg, weights: dict, use_graph: bool = True,
-                 split_len: int = 0, persistent: bool = False):
+                 split_len: int = 0, persistent: bool = False,
+                 one_launch_blocks: bool = False):
         self.rt = rt
         self.cfg = cfg
         self.weights = weights  # keeps the device buffers alive
         c = _abi.LlamaConfig(cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.hidden,
                              cfg.vocab, cfg.max_seq, cfg.theta, cfg.eps, cfg.w_dtype,
-                             cfg.kv_dtype, int(use_graph), split_len, int(persistent))
+                             cfg.kv_dtype, int(use_graph), split_len, int(persistent),
+                             int(one_launch_blocks))
         w = _abi.LlamaWeights(*[ctypes.c_void_p(int(weights[n])) for n in WEIGHT_NAMES])
         h = ctypes.c_void_p()
         call("ammon_llama_create", rt.handle, ctypes.byref(c), ctypes.byref(w), ctypes.byref(h))

@@ -35,6 +35,11 @@ typedef struct ammon_llama_config {
   uint32_t persistent;  /* run each token as one persistent cooperative kernel
                            (bf16 weights, head 128, q heads per kv head in
                            {1, 2, 4, 8}); other shapes use the launch list */
+  uint32_t one_launch_blocks; /* 1: record each attention / SwiGLU block as one
+                                 launch (ammon_attention_block,
+                                 ammon_swiglu_block) where the shape allows;
+                                 same results as the separate launches, which
+                                 measured faster on MI355X (the default) */
 } ammon_llama_config;
 
 typedef struct ammon_llama_weights {

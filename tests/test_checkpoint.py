@@ -32,6 +32,20 @@ def test_probe_reads_the_header(tmp_path, weights, version, shared):
     assert size == path.stat().st_size
 
 
+def test_probe_sizes_need_64_bit_arithmetic(tmp_path):
+    # dim 65536: dim * dim is 2^32, which a 32-bit product wraps to 0.  The
+    # legacy layout (negative vocab: separate classifier) needs
+    # 4 * (V D + 2 L D + D + L (D D + 2 kvd D + D D + 3 H D) + seq head + V D)
+    # bytes after the 28-byte header.
+    D, H, L, heads, kv, V, S = 65536, 8, 1, 1, 1, 3, 2
+    p = tmp_path / "wide.bin"
+    p.write_bytes(struct.pack("<7i", D, H, L, heads, kv, -V, S))
+    kvd = D // heads * kv
+    floats = V * D + 2 * L * D + D + L * (D * D + 2 * kvd * D + D * D + 3 * H * D) + S * D + V * D
+    _, _, shared, size = probe_checkpoint(str(p))
+    assert not shared and size == 28 + 4 * floats
+
+
 def test_probe_rejections(tmp_path):
     p = tmp_path / "bad.bin"
     p.write_bytes(struct.pack("<Ii", llama2c.MAGIC, 2) + b"\0" * 300)

@@ -295,6 +295,37 @@ def test_attention_prefill_equals_decode_per_token(rt, q_heads, kv_heads, head, 
         assert rel_err(got[t], want) <= RTOL
 
 
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+def test_attention_prefill_positions_past_ctx_are_poisoned(rt, kv_dtype):
+    # The grid and the scratch cover ctx positions; the host cannot see
+    # step->position, so a token at position >= ctx (but < seq) must get NaN
+    # and write no partial instead of silently dropping the keys past ctx.
+    q_heads, kv_heads, head, seq, split, T, ctx, p0 = 4, 2, 64, 64, 8, 6, 20, 17
+    kc_pm = oracle.storage(oracle.normal(seq * kv_heads * head, 251), kv_dtype).reshape(
+        seq, kv_heads, head)
+    vc_pm = oracle.storage(oracle.normal(seq * kv_heads * head, 252), kv_dtype).reshape(
+        seq, kv_heads, head)
+    qh = oracle.normal(T * q_heads * head, 253).reshape(T, q_heads, head)
+    kc, vc = up(rt, head_major(kc_pm, kv_heads, seq, head)), up(rt, head_major(vc_pm, kv_heads, seq, head))
+    q, out = up(rt, qh), rt.alloc(T * q_heads * head * 4)
+    nbytes = _abi.lib.ammon_attention_prefill_scratch_bytes(T, q_heads, head, ctx, split)
+    part_h = np.full(nbytes // 4, 7.0, np.float32)  # a sentinel no write leaves
+    part = up(rt, part_h)
+    step = rt.step(0, p0)
+    call("ammon_attention_prefill", rt.handle, None, q, T, q_heads, kc, vc, kv_dtype, kv_heads,
+         head, seq, step, ctx, split, part, nbytes, out)
+    got = out.download((T, q_heads, head))
+    live = ctx - p0  # tokens at positions p0 .. ctx - 1
+    for t in range(live):
+        want = oracle.attention(qh[t], kc_pm, vc_pm, kv_dtype, p0 + t)
+        assert rel_err(got[t], want) <= RTOL, t
+    assert np.isnan(got[live:]).all()
+    splits = _abi.lib.ammon_attention_splits(ctx, split)
+    per_token = q_heads * splits * (head + 2)
+    after = part.download(nbytes // 4)
+    np.testing.assert_array_equal(after[live * per_token:], 7.0)
+
+
 def test_attention_prefill_validation(rt):
     q = up(rt, np.zeros((2, 2, 64), np.float32))
     kc = up(rt, np.zeros((1, 16, 64), np.float32))
