@@ -101,7 +101,7 @@ struct GemvPass {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const uint32_t c = t * tile_chunks + u * 64 + lane;
-        buf[k][u] = C::load_buf(r, c * (uint32_t)(CH * sizeof(WT)));
+        buf[k][u] = C::template load_buf<AMMON_WEIGHT_CPOL>(r, c * (uint32_t)(CH * sizeof(WT)));
       }
     }
   }
