@@ -2,10 +2,24 @@
 // units in attention_impl.h: pass 1 on a (splits, kv heads) grid, pass 2 on
 // a (q heads, head / 32) grid; a z dimension runs consecutive query tokens
 // (prefill).
+//
+// Every kernel takes the DecodeStep pointer first, as a scalar argument that
+// this code object asks to have preloaded into SGPRs at wave launch
+// (-amdgpu-kernarg-preload-count): the position load, which every request of
+// the unit waits for, then goes out without a kernel-argument load before it.
+// The parameter struct follows (its copy of the pointer is ignored).
 #include "attention_impl.h"
 
+#define ATT_KERNEL(NAME) \
+  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(const ammon_k_step *step, \
+                                                             ammon_k_attention p_)
+#define ATT_PARAMS(p0)     \
+  ammon_k_attention p0 = p_; \
+  p0.step = step
+
 #define ATT_PARTIAL(NAME, KV, CH, GMAX, HEAD, EXACT)                             \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p0) { \
+  ATT_KERNEL(NAME) {                                                            \
+    ATT_PARAMS(p0);                                                             \
     __shared__ float lds[att_lds_floats(GMAX, CH)];                             \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                \
     AttnPartial<KV, CH, GMAX, HEAD, EXACT> unit;                                \
@@ -40,7 +54,8 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 // us faster per launch at positions 1023..8191 (four buffers no faster than
 // two)
 #define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_attention p0) { \
+  ATT_KERNEL(NAME) {                                                                \
+    ATT_PARAMS(p0);                                                                 \
     __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                    \
     AttnPartialMfma<GMAX, NBUF> unit;                                               \
@@ -53,15 +68,16 @@ ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 2)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 
-extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine(ammon_k_attention p) {
+ATT_KERNEL(ammon_attention_combine) {
+  ATT_PARAMS(p);
   __shared__ float lds[COMB_LDS_FLOATS];
   attention_combine_unit(attention_token(p, blockIdx.z), blockIdx.x, blockIdx.y, lds);
 }
 
 // Pass 2 for many query tokens: grid (ceil(q_heads / 4), 1, tokens), one
 // wave per (token, q head); the same arithmetic as ammon_attention_combine.
-extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_attention_combine_waves(
-    ammon_k_attention p) {
+ATT_KERNEL(ammon_attention_combine_waves) {
+  ATT_PARAMS(p);
   const ammon_k_attention t = attention_token(p, blockIdx.z);
   const uint32_t h = blockIdx.x * AMMON_WAVES + (threadIdx.x >> 6);
   if (h < t.q_heads) attention_combine_wave(t, h);

@@ -359,14 +359,16 @@ struct AttnPartialMfma {
     return true;
   }
 
+  // Lanes of score columns h >= GMAX load head 0's q: those columns are
+  // never stored, and unconditional loads leave no branch whose join would
+  // wait for the first loads before the K/V requests go out.
   AMMON_DEV void load_q(const ammon_k_attention &p) {
     const uint32_t h = lane & 15;
-    const bool ok = h < GMAX;
-    const float *qp = p.q + (size_t)(g * GMAX + (ok ? h : 0)) * HEAD + 32 * (lane >> 4);
+    const float *qp = p.q + (size_t)(g * GMAX + (h < GMAX ? h : 0)) * HEAD + 32 * (lane >> 4);
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      qraw[kk][0] = ok ? ld_in4(qp + 8 * kk) : make_float4(0.f, 0.f, 0.f, 0.f);
-      qraw[kk][1] = ok ? ld_in4(qp + 8 * kk + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+      qraw[kk][0] = ld_in4(qp + 8 * kk);
+      qraw[kk][1] = ld_in4(qp + 8 * kk + 4);
     }
   }
 
@@ -377,6 +379,9 @@ struct AttnPartialMfma {
     load_q(p);
 #pragma unroll
     for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b]);
+    // keep run()'s q conversion below the requests: scheduled among them,
+    // it waited for q before the later K/V requests went out
+    __builtin_amdgcn_sched_barrier(0);
     return true;
   }
 
@@ -604,28 +609,21 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
   const uint32_t head = p.head, slot = head + 2;
   const uint32_t d0 = slice * SLICE;
   float *out = p.out + (size_t)h * head;
-  const uint32_t pos = p.step->position + p.pos_add;
-  if (pos >= p.limit) {
-    if (threadIdx.x < SLICE && d0 + threadIdx.x < head)
-      st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));
-    return;
-  }
-  const uint32_t live = min(pos / p.split_len + 1, p.splits);
   const float *base = p.partial + (size_t)h * p.splits * slot;
   const uint32_t sl = threadIdx.x >> 2;         // split lane, 0..63
   const uint32_t dq = (threadIdx.x & 3) * DQ;  // DQ dims of the slice
-
-  float a[DQ];
-#pragma unroll
-  for (int k = 0; k < DQ; ++k) a[k] = 0.f;
-  float l = 0.f;
-  if (live <= COMB_ROUNDS * COMB_SPLIT_LANES) {
-    float mv[COMB_ROUNDS], lv[COMB_ROUNDS], dv[COMB_ROUNDS][DQ];
+  // With at most COMB_ROUNDS * 64 splits in the buffer, every split's max,
+  // sum and dims are requested before the position is known (entries of
+  // dead splits are loaded and then ignored), so the position load and the
+  // partials take one round trip instead of two.
+  const bool one_trip = p.splits <= COMB_ROUNDS * COMB_SPLIT_LANES;
+  float mv[COMB_ROUNDS], lv[COMB_ROUNDS], dv[COMB_ROUNDS][DQ];
+  if (one_trip) {
 #pragma unroll
     for (int r = 0; r < COMB_ROUNDS; ++r) {
       const uint32_t s = sl + r * COMB_SPLIT_LANES;
-      const float *row = base + (size_t)(s < live ? s : 0) * slot;
-      mv[r] = s < live ? ld_in(row + head) : -INFINITY;
+      const float *row = base + (size_t)(s < p.splits ? s : 0) * slot;
+      mv[r] = ld_in(row + head);
       lv[r] = ld_in(row + head + 1);
 #pragma unroll
       for (int k = 0; k < DQ; ++k) {
@@ -633,6 +631,23 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
         dv[r][k] = d < head ? ld_in(row + d) : 0.f;
       }
     }
+  }
+  const uint32_t pos = p.step->position + p.pos_add;
+  if (pos >= p.limit) {
+    if (threadIdx.x < SLICE && d0 + threadIdx.x < head)
+      st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));
+    return;
+  }
+  const uint32_t live = min(pos / p.split_len + 1, p.splits);
+
+  float a[DQ];
+#pragma unroll
+  for (int k = 0; k < DQ; ++k) a[k] = 0.f;
+  float l = 0.f;
+  if (one_trip) {
+#pragma unroll
+    for (int r = 0; r < COMB_ROUNDS; ++r)
+      if (sl + r * COMB_SPLIT_LANES >= live) mv[r] = -INFINITY;
     float m = mv[0];
 #pragma unroll
     for (int r = 1; r < COMB_ROUNDS; ++r) m = fmaxf(m, mv[r]);
