@@ -1,9 +1,18 @@
 """Writes tests/golden/c4_greedy.npz: the Llama-3-8B-shaped greedy decode
 (32 layers, dim 4096, 32 q / 8 kv heads of 128, SwiGLU hidden 14336, vocab
 128256, RoPE theta 500000, bf16 weights N(0, 0.02) from the oracle's seeded
-generator, RMSNorm weights 1, bf16 KV cache sized 8192) run through the
-oracle from a seeded 16-token prompt with max_new_tokens 528: 527 steps, 15
-forced prompt tokens then 512 greedy picks (reference src/generate.rs:43-91).
+generator, RMSNorm weights 1, KV cache sized 8192) run through the oracle
+from a seeded 16-token prompt with max_new_tokens 528: 527 steps, 15 forced
+prompt tokens then 512 greedy picks (reference src/generate.rs:43-91).
+
+The KV cache is fp32, as in the reference (src/modules.rs:53-54): greedy
+tokens are compared bit for bit in fp32.  With a bf16 cache, two correct
+implementations whose fp32 K/V differ only by summation order store some
+elements one bf16 ulp apart (2^-8 relative), and 32 random-init layers
+amplify those flips over hundreds of steps until a top-2 margin of 4e-3
+flipped (measured).  The prompt seed is the one of 1004..1027 whose run has
+the widest smallest top-2 margin over the 512 generated steps (2.5e-3 on the
+GPU path), so the comparison is not decided by a near tie.
 
 Stored:
   inputs   config, weight seed, prompt, max_new_tokens, and per weight tensor
@@ -35,14 +44,14 @@ import oracle  # noqa: E402
 C4 = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, hidden=14336, vocab=128256,
           max_seq=8192, theta=500000.0, eps=1e-5)
 WEIGHT_SEED = 1003
-PROMPT_SEED = 1004
+PROMPT_SEED = 1021
 PROMPT_LEN = 16
 MAX_NEW_TOKENS = 528
 PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c4_greedy.npz")
 
 
 def config():
-    return oracle.LlamaConfig(**C4, w_dtype=oracle.BF16, kv_dtype=oracle.BF16)
+    return oracle.LlamaConfig(**C4, w_dtype=oracle.BF16, kv_dtype=oracle.F32)
 
 
 def c4_prompt():
@@ -103,6 +112,7 @@ if __name__ == "__main__":
     prompt, tokens, logits, margins, runners, sums = run()
     np.savez_compressed(PATH, prompt=prompt, tokens=tokens, logits=logits, margins=margins,
                         runners=runners, config=json.dumps(C4), weight_seed=WEIGHT_SEED,
+                        w_dtype=oracle.BF16, kv_dtype=oracle.F32,
                         max_new_tokens=MAX_NEW_TOKENS,
                         checksums=json.dumps({k: [str(s), str(x)] for k, (s, x) in sums.items()}))
     gen = margins[PROMPT_LEN - 1:]
