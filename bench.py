@@ -50,7 +50,7 @@ def token_bytes(c, ctx):
     return weights + kv_read
 
 
-def kernel_bytes(c, ctx):
+def kernel_bytes(c, ctx, split=128):
     """Algorithmic bytes per launch of each per-layer kernel (GEMV: d*n*2 +
     4n + 4d [+ 4d residual]; attention: 2*ctx*kv_dim*2 + q and out)."""
     head = c.dim // c.n_heads
@@ -61,7 +61,14 @@ def kernel_bytes(c, ctx):
         "w2_residual": c.dim * c.hidden * 2 + 4 * c.hidden + 4 * c.dim * 2,
         "wo_residual": c.dim * q * 2 + 4 * q + 4 * c.dim * 2,
         "attention_partial": 2 * ctx * kv * 2 + 8 * q,
+        # the merge reads each live split's (acc, m, l) once and writes out
+        "attention_combine": c.n_heads * -(-ctx // split) * (head + 2) * 4 + 4 * q,
         "lm_head": c.vocab * c.dim * 2 + 4 * c.dim * 2 + 4 * c.vocab,
+        # one launch per block: the algorithmic bytes of its parts
+        "attention_block": ((q + 2 * kv) * c.dim * 2 + 4 * c.dim * 2 + 4 * q + 2 * 2 * kv)
+                           + (2 * ctx * kv * 2 + 8 * q) + (c.dim * q * 2 + 4 * q + 4 * c.dim * 2),
+        "swiglu_block": (2 * c.hidden * c.dim * 2 + 4 * c.dim * 2 + 4 * c.hidden)
+                        + (c.dim * c.hidden * 2 + 4 * c.hidden + 4 * c.dim * 2),
     }
 
 
@@ -81,12 +88,18 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
     rt.fill_normal(x, F32, c.dim, 5, 900)
     qb, hb, xb = rt.alloc(q * 4), rt.alloc(c.hidden * 4), rt.alloc(q * 4)
     xr = rt.alloc(c.dim * 4)
+    rt.fill_normal(xr, F32, c.dim, 5, 901)
     logits = rt.alloc(c.vocab * 4)
     step = rt.step(1, ctx - 1)
     table = rt.upload(ammon_amd.rope_table_host(c.theta, head, c.max_seq))
     if not split:
         split = int(ammon_amd._abi.lib.ammon_attention_default_split(rt.handle, c.n_kv_heads, c.max_seq))
-    part = rt.alloc(ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split))
+    part_bytes = ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split)
+    part = rt.alloc(part_bytes)
+    att = rt.alloc(q * 4)
+    syncs = [rt.alloc(4 * 640), rt.alloc(4 * 640)]  # barrier words of the one-launch blocks
+    for s in syncs:
+        rt.fill(s, F32, 640, 0.0)
     rt.synchronize()
 
     def w(name, l, per):
@@ -107,6 +120,8 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
         "attention_partial": ("ammon_attention_partial", lambda l: (
             rt.handle, stream, qb, c.n_heads, *kv_ptr(l), BF16, c.n_kv_heads, head, c.max_seq,
             step, split, part)),
+        "attention_combine": ("ammon_attention_combine", lambda l: (
+            rt.handle, stream, part, c.n_heads, head, c.max_seq, step, split, xb)),
         "wo_residual": ("ammon_gemv", lambda l: (
             rt.handle, stream, w("wo", l, c.dim * q), BF16, c.dim, q, xb, xr, xr)),
         "gate_up_swiglu": ("ammon_gate_up_swiglu", lambda l: (
@@ -118,9 +133,18 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
         "lm_head": ("ammon_gemv_rmsnorm", lambda l: (
             rt.handle, stream, x, weights["rms_final"], F32, c.eps, weights["wcls"], BF16,
             c.vocab, c.dim, logits)),
+        "attention_block": ("ammon_attention_block", lambda l: (
+            rt.handle, stream, xr, rms("rms_att", l), F32, c.eps, w("wq", l, q * c.dim),
+            w("wk", l, kv * c.dim), w("wv", l, kv * c.dim), w("wo", l, c.dim * q), BF16, c.dim,
+            c.n_heads, c.n_kv_heads, head, *kv_ptr(l), BF16, c.max_seq, step, table, split, qb,
+            att, part, part_bytes, syncs[0])),
+        "swiglu_block": ("ammon_swiglu_block", lambda l: (
+            rt.handle, stream, xr, rms("rms_ffn", l), F32, c.eps, w("w1", l, c.hidden * c.dim),
+            w("w3", l, c.hidden * c.dim), w("w2", l, c.dim * c.hidden), BF16, c.dim, c.hidden,
+            hb, syncs[1])),
     }
     out = {}
-    nbytes = kernel_bytes(c, ctx)
+    nbytes = kernel_bytes(c, ctx, split)
     timer = Timer(rt)
     for name, (entry, args_of) in launches.items():
         fn = getattr(lib, entry)
@@ -217,10 +241,16 @@ def cpu_baseline(rt, model, c, weights, start_pos, token0, gpu_tokens, budget_s)
                    f"output rows"),
         "seconds": round(sum(times), 2),
         "token_parity": bool(all(agree)), "tokens_compared": n,
+        **cpu_info(),
     }
 
 
 MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+# The kernel with the largest share of the token: the gate/up GEMV + SwiGLU
+# (32 launches per token, 235 MB each at the Llama-3-8B shape).
+DOMINANT = "gate_up_swiglu"
+DOMINANT_NAME = "ammon_gemv_bf16_v_swiglu (gate/up GEMV + SwiGLU, RMSNorm prologue)"
 
 
 def prefill_measure(rt, model, c, prompt_lengths=(16, 512), reps=3):
@@ -315,6 +345,378 @@ def copy_probe(rt, reps=4):
         b.free()
 
 
+def cpu_info():
+    """Host the CPU legs run on: model name, cores this process may use,
+    OMP_NUM_THREADS."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "affinity_cores": len(os.sched_getaffinity(0)),
+            "omp_num_threads": os.environ.get("OMP_NUM_THREADS")}
+
+
+def graph_ms(rt, stream, launch_all, reps=5):
+    """Median ms of one replay of a graph that captures launch_all() on
+    `stream` (events around each replay, after one warm replay)."""
+    from ammon_amd import Timer
+    from ammon_amd._abi import call
+
+    call("ammon_capture_begin", rt.handle, stream)
+    launch_all()
+    graph = ctypes.c_void_p()
+    call("ammon_capture_end", rt.handle, stream, ctypes.byref(graph))
+    timer = Timer(rt)
+    try:
+        call("ammon_graph_launch", rt.handle, graph, stream)
+        samples = []
+        for _ in range(reps):
+            timer.start(stream)
+            call("ammon_graph_launch", rt.handle, graph, stream)
+            timer.stop(stream)
+            samples.append(timer.elapsed_ms())
+    finally:
+        timer.close()
+        call("ammon_graph_destroy", rt.handle, graph)
+    return float(np.median(samples))
+
+
+def cpu_seconds(fn, budget_s, at_least=1):
+    """Seconds per call of fn() on the host: repeated until budget_s (and at
+    least `at_least` calls)."""
+    n, t0 = 0, time.perf_counter()
+    while n < at_least or time.perf_counter() - t0 < budget_s:
+        fn()
+        n += 1
+    return (time.perf_counter() - t0) / n
+
+
+def rate(nbytes, us):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    return {"avg_us": round(us, 3), "bytes": int(nbytes), "gbs": round(gbs, 1),
+            "frac": round(gbs / HBM_PEAK_GBS, 4)}
+
+
+def stream_ceiling(rt, model):
+    """The device's plain streaming-read rate: ammon_checksum (one workgroup
+    per CU sweeping the buffer with nontemporal 16-byte loads, two integer
+    ops per 8 bytes) over slices of the 3.76 GB gate matrix stack.  Per
+    size, a captured graph of back-to-back launches over distinct slices
+    (so no launch finds its bytes in a cache), median of 5 replays: the
+    time a pure read of that many bytes takes as one launch, fixed costs
+    included -- the floor for a kernel of that size."""
+    from ammon_amd._abi import F32, call
+    buf = model.weights["w1"]
+    out = rt.alloc(16)
+    stream = model.stream
+    sizes = {}
+    for nbytes in (33554432, 234881024, 1073741824, buf.nbytes):
+        n = min(buf.nbytes // nbytes, 16)
+
+        def launch_all(nbytes=nbytes, n=n):
+            for i in range(n):
+                call("ammon_checksum", rt.handle, stream, ctypes.c_void_p(int(buf) + i * nbytes),
+                     nbytes, out)
+        # each checksum call first zeroes its two result words with a
+        # one-workgroup fill launch: timed alone and subtracted
+        def fills(n=n):
+            for _ in range(n):
+                call("ammon_fill", rt.handle, stream, out, F32, 4, 0.0)
+        ms = (graph_ms(rt, stream, launch_all) - graph_ms(rt, stream, fills)) / n
+        sizes[str(nbytes)] = rate(nbytes, ms * 1e3)
+        log(f"stream read {nbytes / 2**20:7.0f} MiB: {ms * 1e3:8.2f} us "
+            f"({sizes[str(nbytes)]['gbs']:.0f} GB/s)")
+    r = dict(sizes[str(buf.nbytes)])
+    r["kernel"] = "ammon_checksum (plain streaming read, one workgroup per CU)"
+    r["by_size"] = sizes
+    return r
+
+
+C3_CTX = (1024, 4096, 8192)
+
+
+def c3_attention(rt, stream, cpu_budget):
+    """Single-layer decode attention, 32 q / 8 kv heads of 128, bf16 KV, at
+    position ctx - 1 of a cache of ctx positions: split partials + merge
+    (ammon_attention_decode).  Caches rotate through a 1.07 GB pool (one
+    per launch, a graph of all of them), so no launch reads from cache what
+    an earlier one brought in.  CPU leg: the oracle's split-8 pair on the
+    first cache of the pool; parity: the GPU output against it."""
+    import oracle
+    from ammon_amd import attention_scratch_bytes, kv_unpermute
+    from ammon_amd._abi import BF16, F32, call, lib
+
+    q_heads, kv_heads, head = 32, 8, 128
+    pool_elems = 32 * 2 * kv_heads * 8192 * head  # 32 layers' K and V at 8192
+    pool = rt.alloc(pool_elems * 2)
+    rt.fill_normal(pool, BF16, pool_elems, 7, 300)
+    qh = oracle.normal(q_heads * head, 301).reshape(q_heads, head)
+    q = rt.upload(qh)
+    out = rt.alloc(q_heads * head * 4)
+    rt.synchronize()
+    lines = {}
+    for ctx in C3_CTX:
+        split = int(lib.ammon_attention_default_split(rt.handle, kv_heads, ctx))
+        part_bytes = attention_scratch_bytes(q_heads, head, ctx, split)
+        part = rt.alloc(part_bytes)
+        per = kv_heads * ctx * head  # elements of one K (or V) cache
+        pairs = pool_elems // (2 * per)
+        step = rt.step(0, ctx - 1)
+        ptr = lambda i: ctypes.c_void_p(int(pool) + i * per * 2)
+
+        def launch_all():
+            for i in range(pairs):
+                call("ammon_attention_decode", rt.handle, stream, q, q_heads, ptr(2 * i),
+                     ptr(2 * i + 1), BF16, kv_heads, head, ctx, step, split, part, part_bytes,
+                     out)
+
+        us = graph_ms(rt, stream, launch_all) * 1e3 / pairs
+        nbytes = 2 * ctx * kv_heads * head * 2 + 8 * q_heads * head
+        line = rate(nbytes, us)
+        line.update({"split": split, "launches_timed": pairs})
+        # parity and CPU leg on the pool's first cache
+        call("ammon_attention_decode", rt.handle, stream, q, q_heads, ptr(0), ptr(1), BF16,
+             kv_heads, head, ctx, step, split, part, part_bytes, out)
+        rt.synchronize(stream)
+        got = out.download((q_heads, head))
+        kv = []
+        for i in (0, 1):
+            hm = np.empty((kv_heads, ctx, head), np.uint16)
+            call("ammon_memcpy", rt.handle, hm.ctypes.data, ptr(i), hm.nbytes, 2, None)
+            rt.synchronize()
+            kv.append(kv_unpermute(hm, kv_heads, ctx, head))
+        want = oracle.attention(qh, kv[0], kv[1], BF16, ctx - 1)
+        line["rel_err_vs_oracle"] = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+        s = cpu_seconds(lambda: oracle.attention(qh, kv[0], kv[1], BF16, ctx - 1), cpu_budget)
+        line["cpu_us"] = round(s * 1e6, 1)
+        lines[str(ctx)] = line
+        part.free()
+        log(f"C3 ctx {ctx}: {us:.2f} us ({line['gbs']:.0f} GB/s, frac {line['frac']:.3f}); "
+            f"cpu {s * 1e6:.0f} us; rel err {line['rel_err_vs_oracle']:.1e}")
+    pool.free()
+    return {"workload": "single-layer decode attention, 32 q / 8 kv heads of 128, bf16 KV, "
+                        "position ctx - 1; partials + merge per launch", "ctx": lines}
+
+
+def c2_kernels(rt, stream, tok_emb, cpu_budget):
+    """The isolated kernels: embedding gather of 4096 ids from the 128256 x
+    4096 table (bf16 and fp32; 32 id sets per timed graph), RMSNorm over 64
+    and 1 rows of 4096 (eps 1e-5; inputs rotated through a 1 GiB pool), RoPE
+    (theta 500000) of Q [32 x 128] and K [8 x 128] with the cache store at 64
+    random positions, SwiGLU over 14336.  The last two move kilobytes: their
+    times are launch latency, not bandwidth."""
+    import oracle
+    from ammon_amd import rope_table_host
+    from ammon_amd._abi import BF16, F32, call
+
+    out = {}
+    vocab, dim, rows = 128256, 4096, 4096
+    rng = np.random.default_rng(1002)
+    id_sets = [rt.upload(rng.integers(0, vocab, rows).astype(np.uint32)) for _ in range(32)]
+    x = rt.alloc(rows * dim * 4)
+    tab32 = rt.alloc(vocab * dim * 4)
+    rt.fill_normal(tab32, F32, vocab * dim, 9, 1)
+    rt.synchronize()
+    host_bf16 = tok_emb.download(vocab * dim, np.uint16).reshape(vocab, dim)
+    host_ids = id_sets[0].download(rows, np.uint32)
+    for name, table, dt, es in (("embed_bf16", tok_emb, BF16, 2), ("embed_f32", tab32, F32, 4)):
+        def launch_all(table=table, dt=dt):
+            for ids in id_sets:
+                call("ammon_embed_rows", rt.handle, stream, table, dt, vocab, dim, ids, rows, x)
+        us = graph_ms(rt, stream, launch_all) * 1e3 / len(id_sets)
+        out[name] = rate(rows * dim * (es + 4) + 4 * rows, us)
+        if dt == BF16:
+            call("ammon_embed_rows", rt.handle, stream, table, dt, vocab, dim, id_sets[0], rows, x)
+            rt.synchronize(stream)
+            got = x.download((rows, dim))
+            want = oracle.embed(host_bf16, BF16, host_ids)
+            out[name]["bit_exact_vs_oracle"] = bool(np.array_equal(got, want))
+            s = cpu_seconds(lambda: oracle.embed(host_bf16, BF16, host_ids), cpu_budget)
+            out[name]["cpu_us"] = round(s * 1e6, 1)
+    tab32.free()
+    del host_bf16
+    # RMSNorm, in place over slices of a 1 GiB pool
+    pool_floats = 1 << 28
+    pool = rt.alloc(pool_floats * 4)
+    rt.fill_normal(pool, F32, pool_floats, 9, 2)
+    w = rt.alloc(dim * 4)
+    rt.fill_normal(w, F32, dim, 9, 3, 1.0, 0.2)
+    rt.synchronize()
+    for nrows in (64, 1):
+        # at most 1024 launches per graph, spread over the whole pool
+        n = min(pool_floats // (nrows * dim), 1024)
+        stride = pool_floats // n * 4
+        sl = lambda i, stride=stride: ctypes.c_void_p(int(pool) + i * stride)
+
+        def launch_all(n=n, nrows=nrows, sl=sl):
+            for i in range(n):
+                call("ammon_rmsnorm", rt.handle, stream, sl(i), w, F32, sl(i), nrows, dim, 1e-5)
+        us = graph_ms(rt, stream, launch_all, reps=3) * 1e3 / n
+        out[f"rmsnorm_{nrows}x{dim}"] = rate(nrows * dim * 8 + dim * 4, us)
+    xh = oracle.normal(64 * dim, 9).reshape(64, dim)
+    wh = oracle.normal(dim, 10, mean=1.0, std=0.2)
+    out[f"rmsnorm_64x{dim}"]["cpu_us"] = round(
+        cpu_seconds(lambda: oracle.rmsnorm(xh, wh), cpu_budget) * 1e6, 1)
+    pool.free()
+    # RoPE + K store, SwiGLU: launch-latency bound
+    q_heads, kv_heads, head, seq = 32, 8, 128, 8192
+    table = rt.upload(rope_table_host(500000.0, head, seq))
+    qb = rt.alloc(q_heads * head * 4)
+    kp = rt.alloc(kv_heads * head * 4)
+    kc = rt.alloc(kv_heads * seq * head * 2)
+    rt.fill_normal(qb, F32, q_heads * head, 9, 4)
+    rt.fill_normal(kp, F32, kv_heads * head, 9, 5)
+    steps = [rt.step(0, int(p)) for p in rng.integers(0, seq, 64)]
+
+    def rope_all():
+        for st in steps:
+            call("ammon_rope_store", rt.handle, stream, qb, q_heads, kp, kv_heads, head, kc, BF16,
+                 seq, st, table)
+    us = graph_ms(rt, stream, rope_all) * 1e3 / len(steps)
+    out["rope_store"] = rate(4 * q_heads * head * 2 + 4 * kv_heads * head + 2 * kv_heads * head,
+                             us)
+    hb = rt.alloc(14336 * 4)
+    hb2 = rt.alloc(14336 * 4)
+    rt.fill_normal(hb, F32, 14336, 9, 6)
+    rt.fill_normal(hb2, F32, 14336, 9, 7)
+
+    def swiglu_all():
+        for _ in range(64):
+            call("ammon_swiglu", rt.handle, stream, hb, hb2, 14336)
+    us = graph_ms(rt, stream, swiglu_all) * 1e3 / 64
+    out["swiglu_14336"] = rate(3 * 4 * 14336, us)
+    g = oracle.normal(14336, 11)
+    u = oracle.normal(14336, 12)
+    out["swiglu_14336"]["cpu_us"] = round(cpu_seconds(lambda: oracle.swiglu(g, u), cpu_budget) * 1e6,
+                                          1)
+    for k, v in out.items():
+        log(f"C2 {k}: {v['avg_us']:.2f} us ({v['gbs']:.0f} GB/s)"
+            + (f"; cpu {v['cpu_us']:.0f} us" if "cpu_us" in v else ""))
+    return {"workload": "isolated kernels: embed 4096 ids of 128256 x 4096, RMSNorm 64 and 1 "
+                        "rows x 4096, RoPE + K store (32/8 heads of 128), SwiGLU 14336",
+            "kernels": out}
+
+
+C1 = dict(dim=288, n_layers=6, n_heads=6, n_kv_heads=6, hidden=768, vocab=32000, max_seq=256,
+          theta=10000.0, eps=1e-5)
+
+
+def c1_decode(rt, cpu_budget):
+    """The tiny fp32 decoder (dim 288, 6 layers, 6 heads of 48, SwiGLU 768,
+    vocab 32000), seeded 8-token prompt, max_new_tokens 256: 255 greedy steps
+    by the reference's loop on the device (tokens/s with the reference's
+    formula) and by the oracle on the host from the same weights."""
+    import oracle
+    from ammon_amd import LlamaModel
+    from ammon_amd._abi import F32
+
+    c = Cfg(**C1, w_dtype=F32, kv_dtype=F32)
+    m = LlamaModel.synthetic(rt, c, seed=1000, std=0.02)
+    prompt = np.random.default_rng(1001).integers(1, c.vocab, 8).astype(np.int32)
+    m.generate_tokens_device(prompt, 256)  # warm: graph capture
+    toks, _, tps = m.generate_tokens_device(prompt, 256)
+    toks_h, _, tps_h = m.generate_tokens(prompt, 256)
+    host = {}
+    shapes = oracle.weight_shapes(oracle.LlamaConfig(**{k: C1[k] for k in (
+        "dim", "n_layers", "n_heads", "n_kv_heads", "hidden", "vocab", "max_seq")}))
+    for name, buf in m.weights.items():
+        host[name] = buf.download(shapes[name], np.float32)
+    m.close()
+    om = oracle.Model(oracle.LlamaConfig(**C1), host)
+    t0 = time.perf_counter()
+    want, _ = om.generate_tokens(prompt, 256)
+    cpu_s = time.perf_counter() - t0
+    om.close()
+    line = {"tokens_per_s_device_loop": round(tps, 1), "tokens_per_s_host_loop": round(tps_h, 1),
+            "steps": 255, "token_parity": bool(np.array_equal(toks, want) and
+                                                np.array_equal(toks_h, want)),
+            "cpu": {"tokens_per_s": round(255 / cpu_s, 1), "seconds": round(cpu_s, 2),
+                    "cores": oracle.num_threads(), "kind": "port",
+                    "sample": "the full 255-step greedy run"}}
+    log(f"C1: {tps:.0f} tok/s device loop, {tps_h:.0f} host loop; cpu {255 / cpu_s:.1f} tok/s; "
+        f"parity {line['token_parity']}")
+    return line
+
+
+C5 = dict(dim=8192, n_layers=1, n_heads=64, n_kv_heads=8, hidden=28672, vocab=128256,
+          max_seq=32768, theta=500000.0, eps=1e-5)
+
+
+def c5_layer(rt, cpu_budget, steps=16):
+    """One Llama-3-70B-shaped layer + final norm + LM head, bf16 weights and
+    KV, the cache prefilled N(0, 1): greedy decode steps at positions
+    32752..32767 as one graph per step; ms per step against the HBM roofline
+    of its bytes.  CPU leg: the oracle on the same weights and cache, a few
+    steps from 32752, with token parity."""
+    import oracle
+    from ammon_amd import LlamaModel, Timer, kv_unpermute
+    from ammon_amd._abi import BF16, F32, call
+
+    c = Cfg(**C5, w_dtype=BF16, kv_dtype=BF16)
+    head = c.dim // c.n_heads
+    m = LlamaModel.synthetic(rt, c, seed=70, std=0.02)
+    for i, name in enumerate(("rms_att", "rms_ffn", "rms_final")):
+        rt.fill_normal(m.weights[name], F32, c.dim, 71, i, 1.0, 0.2)
+    kv_n = c.n_kv_heads * c.max_seq * head
+    k, v = ctypes.c_void_p(), ctypes.c_void_p()
+    call("ammon_llama_kv_layer", m.handle, 0, ctypes.byref(k), ctypes.byref(v))
+    rt.fill_normal(k, BF16, kv_n, 72, 0)
+    rt.fill_normal(v, BF16, kv_n, 72, 1)
+    rt.synchronize()
+    start = c.max_seq - steps
+    m.decode(128000, start - 8, 8)  # warm: graph capture
+    timer = Timer(rt)
+    timer.start(m.stream)
+    m.decode(128000, start, steps)
+    timer.stop(m.stream)
+    ms = timer.elapsed_ms() / steps
+    timer.close()
+    gpu_tokens = m.read_tokens(start, steps)
+    nbytes = token_bytes(c, c.max_seq - steps // 2)
+    line = {"ms_per_step": round(ms, 4), "step_bytes": nbytes,
+            "roofline_ms": round(nbytes / (HBM_PEAK_GBS * 1e9) * 1e3, 4),
+            "gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}
+    if cpu_budget > 0:
+        shapes = oracle.weight_shapes(oracle.LlamaConfig(**{kk: C5[kk] for kk in (
+            "dim", "n_layers", "n_heads", "n_kv_heads", "hidden", "vocab", "max_seq")}))
+        host = {}
+        for name, buf in m.weights.items():
+            dt = np.float32 if name.startswith("rms") else np.uint16
+            host[name] = buf.download(shapes[name], dt)
+        om = oracle.Model(oracle.LlamaConfig(**C5, w_dtype=BF16, kv_dtype=BF16), host)
+        for src, get in ((k, oracle._lib.orc_model_key_cache), (v, oracle._lib.orc_model_value_cache)):
+            hm = np.empty((c.n_kv_heads, c.max_seq, head), np.uint16)
+            call("ammon_memcpy", rt.handle, hm.ctypes.data, src, hm.nbytes, 2, None)
+            rt.synchronize()
+            pm = kv_unpermute(hm, c.n_kv_heads, c.max_seq, head)
+            ctypes.memmove(get(om._handle, 0), pm.ctypes.data, pm.nbytes)
+        # the GPU decode from `start` began with token 128000
+        tok, toks, times = 128000, [], []
+        for pos in range(start, c.max_seq):
+            t0 = time.perf_counter()
+            logits = om.step(tok, pos)
+            times.append(time.perf_counter() - t0)
+            tok = int(oracle.sample_argmax(logits))
+            toks.append(tok)
+            if sum(times) > cpu_budget:
+                break
+        om.close()
+        line["cpu"] = {"ms_per_step": round(1e3 * sum(times) / len(times), 1),
+                       "steps": len(times), "cores": oracle.num_threads(), "kind": "port",
+                       "token_parity": bool(np.array_equal(toks, gpu_tokens[: len(toks)]))}
+    m.close()
+    log(f"C5: {ms:.3f} ms/step (roofline {line['roofline_ms']:.3f} ms, frac {line['frac']:.3f})"
+        + (f"; cpu {line['cpu']['ms_per_step']:.0f} ms/step, parity {line['cpu']['token_parity']}"
+           if "cpu" in line else ""))
+    return line
+
+
 def oracle_layout(head_major, kv_heads, seq, head):
     from ammon_amd import kv_unpermute
     return kv_unpermute(head_major.reshape(kv_heads, seq, head), kv_heads, seq, head)
@@ -335,6 +737,8 @@ def main():
     ap.add_argument("--split", type=int, default=0,
                     help="attention split length (0: the library's choice)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prompt-prefill lines")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the other workloads' lines (C1, C2, C3, C5) and the stream ceiling")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain streaming kernel of known size (ammon_add over "
                          "256 MiB operands), the calibration for HBM byte counters")
@@ -403,8 +807,8 @@ def main():
                            use_graph=not args.no_graph)
     for k, v in kernels.items():
         log(f"  {k:18s} {v['avg_us']:9.2f} us  {v['gbs']:7.1f} GB/s  frac {v['frac']:.3f}")
-    dom = kernels["gate_up_swiglu"]
-    traffic = measured_traffic("gate_up_swiglu", dom["bytes"])
+    dom = kernels[DOMINANT]
+    traffic = measured_traffic(DOMINANT, dom["bytes"])
 
     cpu = None
     if args.cpu_budget > 0 and not args.no_cpu:
@@ -414,6 +818,22 @@ def main():
 
     # after the CPU baseline: prefill rewrites the first cache positions
     prefill = None if args.no_prefill else prefill_measure(rt, model, c)
+
+    # the other workloads, each with its CPU leg (not part of `value`)
+    extras = {}
+    if not args.no_configs:
+        cb = 0.0 if args.no_cpu else args.cpu_budget
+        small = 0.5 if cb > 0 else 0.0
+        for name, fn in (("stream_read_ceiling", lambda: stream_ceiling(rt, model)),
+                         ("c3", lambda: c3_attention(rt, stream, small)),
+                         ("c2", lambda: c2_kernels(rt, stream, model.weights["tok_emb"], small)),
+                         ("c1", lambda: c1_decode(rt, cb)),
+                         ("c5", lambda: c5_layer(rt, min(cb, 10.0)))):
+            try:
+                extras[name] = fn()
+            except Exception as e:  # recorded in the JSON line; the headline stands
+                extras[name] = {"error": f"{type(e).__name__}: {e}"}
+                log(f"{name} failed: {extras[name]['error']}")
 
     result = {
         "metric": METRIC,
@@ -443,7 +863,7 @@ def main():
                                          4),
         },
         "roofline": {
-            "kernel": "ammon_gemv_bf16_v_swiglu (gate/up GEMV + SwiGLU, RMSNorm prologue)",
+            "kernel": DOMINANT_NAME,
             "bound": "hbm",
             "achieved": dom["gbs"],
             "peak": HBM_PEAK_GBS,
@@ -457,6 +877,8 @@ def main():
         "kernels": kernels,
         "prefill": prefill,
         "cpu_baseline": cpu,
+        "stream_read_ceiling": extras.get("stream_read_ceiling"),
+        "configs": {k: extras[k] for k in ("c1", "c2", "c3", "c5") if k in extras},
     }
     model.close()
     print(json.dumps(result), flush=True)
