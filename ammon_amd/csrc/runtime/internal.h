@@ -90,6 +90,11 @@ ammon_status set_error(ammon_status st, const char *fmt, ...)
     __attribute__((format(printf, 2, 3)));
 ammon_status hip_error(hipError_t e, const char *what);
 
+// Looks up this device's copy of the library scratch used by
+// ammon_attention_decode_noalloc (runtime/noalloc.hip); call once per device
+// with that device current.
+ammon_status noalloc_init(int device);
+
 }  // namespace ammon_rt
 
 struct ammon_runtime {

@@ -226,6 +226,7 @@ static ammon_status create(int device, ammon_runtime **out) {
     if (v > 0 && v <= 64) rt->gemv_wgs_per_cu = (uint32_t)v;
   }
   ammon_status st = load_kernels(rt);
+  if (st == AMMON_OK) st = noalloc_init(device);  // device is current
   if (st == AMMON_OK) {
     e = hipStreamCreateWithFlags(&rt->stream, hipStreamNonBlocking);
     if (e != hipSuccess) st = hip_error(e, "hipStreamCreateWithFlags");

@@ -234,6 +234,23 @@ ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, cons
                                     uint32_t split_len, float *partial, size_t partial_bytes,
                                     float *out);
 
+/* No counterpart in the reference.  For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): ammon_attention_decode with the split partials in a
+ * library-owned device array of AMMON_NOALLOC_SCRATCH_BYTES per GPU instead
+ * of a caller buffer.  Same kernels, same results; allocates nothing.  Fails
+ * with AMMON_E_VALIDATION when ammon_attention_scratch_bytes(q_heads, head,
+ * seq, split_len) exceeds the array.  All calls on one GPU share its array:
+ * calls that can overlap on one GPU (unordered streams) race. */
+#define AMMON_NOALLOC_SCRATCH_BYTES (4u << 20)
+ammon_status ammon_attention_decode_noalloc(ammon_runtime *rt, ammon_stream stream,
+                                            const float *q, uint32_t q_heads,
+                                            const void *k_cache, const void *v_cache,
+                                            ammon_dtype kv_dtype, uint32_t kv_heads,
+                                            uint32_t head, uint32_t seq,
+                                            const ammon_decode_step *step, uint32_t split_len,
+                                            float *out);
+
 /* swiglu (reference src/kernels.rs:462-476): hb = silu(hb) * hb2. */
 ammon_status ammon_swiglu(ammon_runtime *rt, ammon_stream stream, float *hb, const float *hb2,
                           uint32_t n);
