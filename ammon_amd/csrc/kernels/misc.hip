@@ -100,7 +100,21 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_checksum(ammon_k_ch
     s += __shfl_xor(s, off, 64);
     x ^= __shfl_xor(x, off, 64);
   }
+  // one atomic pair per workgroup: the waves' sums meet in LDS first (every
+  // atomic on the two result words is serialized at one address)
+  __shared__ unsigned long long ws[AMMON_WAVES], wx[AMMON_WAVES];
+  const uint32_t wave = threadIdx.x >> 6;
   if ((threadIdx.x & 63) == 0) {
+    ws[wave] = s;
+    wx[wave] = x;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+#pragma unroll
+    for (int w = 1; w < AMMON_WAVES; ++w) {
+      s += ws[w];
+      x ^= wx[w];
+    }
     atomicAdd(p.out, s);
     atomicXor(p.out + 1, x);
   }
