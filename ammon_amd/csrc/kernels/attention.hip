@@ -1,6 +1,6 @@
 // attention.hip -- standalone split-K decode attention kernels over the
 // units in attention_impl.h: pass 1 on a (splits, kv heads) grid, pass 2 on
-// a (q heads, head / 32) grid; a z dimension runs consecutive query tokens
+// a (q heads, head / 8) grid; a z dimension runs consecutive query tokens
 // (prefill).
 //
 // Every kernel takes the DecodeStep pointer first, as a scalar argument that
@@ -68,10 +68,12 @@ ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 2)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 
+// Merge units of 8 dims: 512 workgroups at the Llama-3-8B shape (32 q
+// heads); measured 3.7 us per launch against 4.2 for 32-dim units.
 ATT_KERNEL(ammon_attention_combine) {
   ATT_PARAMS(p);
-  __shared__ float lds[COMB_LDS_FLOATS];
-  attention_combine_unit(attention_token(p, blockIdx.z), blockIdx.x, blockIdx.y, lds);
+  __shared__ float lds[COMB_LDS_FLOATS_W(8)];
+  attention_combine_unit<8>(attention_token(p, blockIdx.z), blockIdx.x, blockIdx.y, lds);
 }
 
 // Pass 2 for many query tokens: grid (ceil(q_heads / 4), 1, tokens), one

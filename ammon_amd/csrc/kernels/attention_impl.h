@@ -15,7 +15,7 @@
 // the reference's layout [q_heads, splits, head + 2].  Splits that start past
 // pos write nothing.
 //
-// Pass 2, one workgroup per (q head, 32-dim slice): M = max m_s over live splits,
+// Pass 2, one workgroup per (q head, 8- or 32-dim slice): M = max m_s over live splits,
 // out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
 //
 // The reference uses fixed 8-position splits (src/kernels.rs:228-229); here

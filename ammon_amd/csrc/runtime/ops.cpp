@@ -406,7 +406,7 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
                          ammon_attention_splits(seq, split_len), 0, seq};
-  return launch_att(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 32), 1, p,
+  return launch_att(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 8), 1, p,
                     "attention_combine");
 }
 
