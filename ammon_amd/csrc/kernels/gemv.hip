@@ -36,6 +36,11 @@
   GEMV_KERNEL(PREFIX##_plain_argmax, WT, CH, RPW, U, AMMON_GEMV_PLAIN_ARGMAX)
 
 GEMV_MODES(ammon_gemv_bf16_v, uint16_t, 8, 2, 4)
+// Long bf16 matrices without an epilogue (the LM head): 4 rows per wave
+// (128256 x 4096: 155 vs 160 us per launch; slower for the per-layer
+// projections)
+GEMV_KERNEL(ammon_gemv_bf16_w_plain, uint16_t, 8, 4, 4, AMMON_GEMV_PLAIN)
+GEMV_KERNEL(ammon_gemv_bf16_w_plain_argmax, uint16_t, 8, 4, 4, AMMON_GEMV_PLAIN_ARGMAX)
 GEMV_MODES(ammon_gemv_bf16_s, uint16_t, 1, 2, 4)
 GEMV_MODES(ammon_gemv_f32_v, float, 4, 2, 4)
 GEMV_MODES(ammon_gemv_f32_s, float, 1, 2, 4)

@@ -34,6 +34,7 @@ struct Kernels {
   hipFunction_t att_combine_waves = nullptr;  // one wave per (token, q head)
   hipFunction_t gemv[2][2][kGemvModes] = {};
   hipFunction_t gemv_argmax[2][2] = {};  // PLAIN_ARGMAX: [dtype][vector?]
+  hipFunction_t gemv_wide[2] = {};       // bf16 vector, kGemvWideRowsPerWave: [plain, argmax]
   hipFunction_t swiglu = nullptr;
   hipFunction_t add = nullptr;
   hipFunction_t argmax_partial = nullptr;
@@ -60,6 +61,10 @@ constexpr uint32_t kLdsPerCu = 160 * 1024;
 
 // GEMV rows per wave and waves per workgroup (must match gemv.hip).
 constexpr uint32_t kGemvRowsPerWave = 2;
+// the wide variant (plain / plain_argmax, bf16, 16-byte chunks) for matrices
+// of at least kGemvWideMinRows rows
+constexpr uint32_t kGemvWideRowsPerWave = 4;
+constexpr uint32_t kGemvWideMinRows = 65536;
 constexpr uint32_t kGemvTileChunks = 4;  // U: chunks per lane per tile
 constexpr uint32_t kGemvWaves = 4;
 constexpr uint32_t kWorkgroup = 256;

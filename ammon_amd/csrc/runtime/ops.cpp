@@ -95,6 +95,13 @@ struct GemvArgs {
   uint32_t cand_cap;
 };
 
+// The wide GEMV variant applies: a long bf16 matrix in 16-byte chunks with
+// no epilogue beyond the argmax candidates.
+static bool gemv_wide(const GemvArgs &a, int vec_ok) {
+  return vec_ok && a.w_dtype == AMMON_BF16 && a.rows >= kGemvWideMinRows &&
+         (a.mode == AMMON_GEMV_PLAIN || a.mode == AMMON_GEMV_PLAIN_ARGMAX);
+}
+
 // Validates and packs a GEMV: *p receives the kernel parameters, *lds_out
 // the bytes of LDS its x staging needs, *vec_out whether the 16-byte-chunk
 // (vector) kernels apply.
@@ -138,7 +145,8 @@ ammon_status gemv_pack(ammon_runtime *rt, const GemvArgs &a, const char *what, a
   p.d = a.d;
   p.n = a.n;
   p.rows = a.rows;
-  const uint32_t rows_per_wg = kGemvRowsPerWave * kGemvWaves;
+  const uint32_t rows_per_wg =
+      (gemv_wide(a, vec_ok) ? kGemvWideRowsPerWave : kGemvRowsPerWave) * kGemvWaves;
   p.row_blocks = cdiv(a.rows, rows_per_wg);
   p.norm_dtype = (uint32_t)a.norm_dtype;
   p.eps = a.eps;
@@ -170,8 +178,9 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   // bounds it); among 2..max per CU pick the count whose grid-stride split of
   // the row blocks wastes the least (blocks / (grid * blocks per workgroup)).
   const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
-  hipFunction_t fn = a.mode == AMMON_GEMV_PLAIN_ARGMAX ? rt->k.gemv_argmax[dt][vec]
-                                                      : rt->k.gemv[dt][vec][a.mode];
+  hipFunction_t fn = gemv_wide(a, vec)                  ? rt->k.gemv_wide[a.mode == AMMON_GEMV_PLAIN_ARGMAX]
+                     : a.mode == AMMON_GEMV_PLAIN_ARGMAX ? rt->k.gemv_argmax[dt][vec]
+                                                         : rt->k.gemv[dt][vec][a.mode];
   const uint32_t resident = occupancy(rt, fn, lds);
   const uint32_t max_per_cu = std::max<uint32_t>(1, std::min(rt->gemv_wgs_per_cu, resident));
   uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * max_per_cu);

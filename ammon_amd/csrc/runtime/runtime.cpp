@@ -134,6 +134,8 @@ static ammon_status load_kernels(ammon_runtime *rt) {
       snprintf(name, sizeof name, "ammon_gemv_%s_%s_plain_argmax", dtn[d], v ? "v" : "s");
       R(4, name, k.gemv_argmax[d][v]);
     }
+  R(4, "ammon_gemv_bf16_w_plain", k.gemv_wide[0]);
+  R(4, "ammon_gemv_bf16_w_plain_argmax", k.gemv_wide[1]);
   R(5, "ammon_swiglu", k.swiglu);
   R(5, "ammon_add", k.add);
   R(5, "ammon_argmax_partial", k.argmax_partial);
