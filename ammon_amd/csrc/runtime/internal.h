@@ -62,9 +62,13 @@ constexpr uint32_t kLdsPerCu = 160 * 1024;
 // GEMV rows per wave and waves per workgroup (must match gemv.hip).
 constexpr uint32_t kGemvRowsPerWave = 2;
 // the wide variant (plain / plain_argmax, bf16, 16-byte chunks) for matrices
-// of at least kGemvWideMinRows rows
+// of at least kGemvWideMinRows rows of at most kGemvWideMaxRowBytes: the LM
+// head at 128256 x 4096 runs 155 against 160 us per launch; at 128256 x
+// 8192 the 2-row kernel (up to four workgroups per CU where the wide one's
+// registers allow two) is ~36 us faster
 constexpr uint32_t kGemvWideRowsPerWave = 4;
 constexpr uint32_t kGemvWideMinRows = 65536;
+constexpr uint64_t kGemvWideMaxRowBytes = 8192;
 constexpr uint32_t kGemvTileChunks = 4;  // U: chunks per lane per tile
 constexpr uint32_t kGemvWaves = 4;
 constexpr uint32_t kWorkgroup = 256;

@@ -99,6 +99,7 @@ struct GemvArgs {
 // no epilogue beyond the argmax candidates.
 static bool gemv_wide(const GemvArgs &a, int vec_ok) {
   return vec_ok && a.w_dtype == AMMON_BF16 && a.rows >= kGemvWideMinRows &&
+         (uint64_t)a.n * 2 <= kGemvWideMaxRowBytes &&
          (a.mode == AMMON_GEMV_PLAIN || a.mode == AMMON_GEMV_PLAIN_ARGMAX);
 }
 
