@@ -282,8 +282,27 @@ struct GemvPass {
         ss = ss / (float)n;
         ss = ss + p.eps;
         const float s = 1.0f / sqrtf(ss);
-        for (uint32_t j = tid; j < n; j += AMMON_WG)
-          xs[xi(j)] = load_elem(p.norm_w, p.norm_dtype, j) * (s * xs[xi(j)]);
+        if (xvec && wvec) {
+          // each lane scales the quads it staged, 16-byte weight loads
+          // several in flight (a scalar pass, one load per element, made the
+          // dim-8192 layer + LM head step 0.662 ms against 0.647)
+#pragma unroll 4
+          for (uint32_t c = tid; c < n / 4; c += AMMON_WG) {
+            float4 w4;
+            if (p.norm_dtype == AMMON_K_BF16) {
+              const uint2 wb = ((const uint2 *)p.norm_w)[c];
+              w4 = make_float4(bf16_lo(wb.x), bf16_hi(wb.x), bf16_lo(wb.y), bf16_hi(wb.y));
+            } else {
+              w4 = ((const float4 *)p.norm_w)[c];
+            }
+            const float4 v = xs4[xq(c)];
+            xs4[xq(c)] = make_float4(w4.x * (s * v.x), w4.y * (s * v.y), w4.z * (s * v.z),
+                                     w4.w * (s * v.w));
+          }
+        } else {
+          for (uint32_t j = tid; j < n; j += AMMON_WG)
+            xs[xi(j)] = load_elem(p.norm_w, p.norm_dtype, j) * (s * xs[xi(j)]);
+        }
       }
     }
     // zero padding up to whole tiles (the matching weight chunks read as 0)

@@ -407,6 +407,26 @@ def test_gemv_rmsnorm_lm_head(rt, d, n):
     assert rel_err(down(y, d), want) <= RTOL
 
 
+@pytest.mark.parametrize("n,g_dtype", [(8192, F32), (8192, BF16), (14336, F32), (8190, F32)])
+def test_gemv_rmsnorm_prologue_matches_separate_norm(rt, n, g_dtype):
+    # Rows longer than the register-staged prologue covers (dim 8192 and up;
+    # 8190 takes the scalar staging): the fused norm normalises x exactly as
+    # ammon_rmsnorm does, so the GEMV outputs are bit-identical.
+    d = 1024
+    wh = oracle.storage(oracle.normal(d * n, 91, std=0.02), BF16).reshape(d, n)
+    xh = oracle.normal(n, 92) * 3
+    gh = oracle.storage(1.0 + 0.1 * oracle.normal(n, 93), g_dtype)
+    w, x, g = up(rt, wh), up(rt, xh), up(rt, gh)
+    y1, y2, xn = rt.alloc(d * 4), rt.alloc(d * 4), rt.alloc(n * 4)
+    call("ammon_gemv_rmsnorm", rt.handle, None, x, g, g_dtype, 1e-5, w, BF16, d, n, y1)
+    call("ammon_rmsnorm", rt.handle, None, x, g, g_dtype, xn, 1, n, 1e-5)
+    call("ammon_gemv", rt.handle, None, w, BF16, d, n, xn, y2, None)
+    got, sep = down(y1, d), down(y2, d)
+    np.testing.assert_array_equal(got.view(np.uint32), sep.view(np.uint32))
+    want = oracle.gemv(wh, BF16, oracle.rmsnorm(xh, gh, g_dtype).reshape(-1))
+    assert rel_err(got, want) <= RTOL
+
+
 def test_gemv_validation(rt):
     x = up(rt, np.zeros(8, np.float32))
     with pytest.raises(AmmonError, match="y overlaps x"):
