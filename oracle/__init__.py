@@ -7,8 +7,8 @@ greedy loop (``src/generate.rs``) and argmax (``src/tokenizer.rs:179-189``),
 citing file:line per function.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s cpu_baseline
-leg may import this package, and only as the checker (or the reported CPU
-baseline).  The product package ``ammon_amd`` never calls it.
+leg may import this package, and only to check results (or as the reported
+CPU baseline).  The product package ``ammon_amd`` never calls it.
 
 Layouts are the reference's: KV cache ``[seq, kv_heads, head]`` per layer,
 weights ``[out, in]`` row-major, attention scratch ``[q_heads, splits,

@@ -1,7 +1,7 @@
 /*
  * ammon_oracle.c -- CPU restatement of koubaa/ammon's decode-layer kernels.
  *
- * TEST INFRASTRUCTURE ONLY: the parity checker for ammon_amd's HIP path and
+ * TEST INFRASTRUCTURE ONLY: the parity reference for ammon_amd's HIP path and
  * the cpu_baseline of bench.py.  Nothing in the product links or calls it.
  *
  * Every function names the reference file:line it restates.  The reference's

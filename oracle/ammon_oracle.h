@@ -1,10 +1,10 @@
 /*
  * ammon_oracle.h -- CPU restatement of koubaa/ammon's decode-layer arithmetic.
  *
- * TEST INFRASTRUCTURE ONLY.  This library is the parity checker for the HIP
- * path in ammon_amd/.  Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py may load it, and only as the checker or as the
- * reported CPU baseline -- never as a product code path.
+ * TEST INFRASTRUCTURE ONLY.  This library is the parity reference for the
+ * HIP path in ammon_amd/.  Only tests/, __graft_entry__.smoke() and the
+ * cpu_baseline leg of bench.py may load it, and only to check results or as
+ * the reported CPU baseline -- never as a product code path.
  *
  * Layouts follow the reference, not the GPU build:
  *   - KV cache per layer is position-major [seq, kv_heads, head]

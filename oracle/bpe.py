@@ -7,7 +7,7 @@ decode) and of the text assembly of ``generate`` (``src/generate.rs:93-118``),
 citing file:line per function.  Strings are handled as UTF-8 ``bytes``, as
 the reference's ``String``s hold them.
 
-Only ``tests/`` may import this module, as the checker; the product
+Only ``tests/`` may import this module, to check results; the product
 (``libammon_amd.so``'s C++ tokenizer) never calls it.
 
 Points where the reference's behaviour comes from Rust's standard library

@@ -1,5 +1,5 @@
 """Pins the CPU oracle (oracle/ammon_oracle.c) before it is trusted as the
-parity checker.
+parity reference.
 
 Each oracle function is checked against something that does not restate it:
 the reference's own known-answer tests (tests/kernels.rs, src/tokenizer.rs),
