@@ -200,7 +200,7 @@ static ammon_status create(int device, ammon_runtime **out) {
   hipDeviceProp_t prop;
   AMMON_HIP(hipGetDeviceProperties(&prop, device));
   if (std::strncmp(prop.gcnArchName, "gfx950", 6) != 0)
-    return set_error(AMMON_E_NO_DEVICE, "device %d is %s; this build targets gfx950 only", device,
+    return set_error(AMMON_E_NO_DEVICE, "device %d is %s; libammon_amd targets gfx950 only", device,
                      prop.gcnArchName);
   ammon_runtime *rt = new ammon_runtime();
   rt->device = device;

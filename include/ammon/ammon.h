@@ -167,7 +167,7 @@ ammon_status ammon_kv_permute(const void *pos_major, void *head_major, uint32_t 
 uint32_t ammon_attention_splits(uint32_t seq, uint32_t split_len);
 size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t seq,
                                      uint32_t split_len);
-/* Split length this build picks for a kv-head count and cache length so that
+/* Split length the library picks for a kv-head count and cache length so that
  * kv_heads * splits fills the device at full context. */
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq);
 

@@ -27,8 +27,8 @@
 
 /* ---- bf16 ------------------------------------------------------------------
  * Round-to-nearest-even truncation of the fp32 pattern; NaN stays NaN (quiet
- * bit set).  The reference is fp32-only; bf16 storage is this build's
- * extension and both sides round with this rule. */
+ * bit set).  The reference is fp32-only; bf16 storage is an extension of
+ * the HIP path, and both sides round with this rule. */
 uint16_t orc_f32_to_bf16(float f) {
   uint32_t u;
   memcpy(&u, &f, 4);
