@@ -395,9 +395,11 @@ def test_gemv_matches_oracle(rt, d, n, w_dtype):
     assert rel_err(down(r, d), rh + want) <= RTOL
 
 
-@pytest.mark.parametrize("d,n", [(128256, 4096), (32000, 288), (4096, 4096)])
+# (65541, 2056): the 4-rows-per-wave kernel (>= 65536 rows of <= 8 KiB) with a
+# ragged last row block and a partial last tile
+@pytest.mark.parametrize("d,n", [(128256, 4096), (32000, 288), (4096, 4096), (65541, 2056)])
 def test_gemv_rmsnorm_lm_head(rt, d, n):
-    w_dtype = BF16 if n == 4096 else F32
+    w_dtype = BF16 if n != 288 else F32
     wh = oracle.storage(oracle.normal(d * n, 81, std=0.02), w_dtype).reshape(d, n)
     xh = oracle.normal(n, 82) * 3
     gh = 1.0 + 0.1 * oracle.normal(n, 83)
@@ -608,7 +610,8 @@ def test_fill_const(rt):
     np.testing.assert_array_equal(down(buf, 1000, np.uint16), 0x3F80)
 
 
-@pytest.mark.parametrize("vocab,dim,w_dtype", [(32000, 288, F32), (128256, 512, BF16)])
+@pytest.mark.parametrize("vocab,dim,w_dtype", [(32000, 288, F32), (128256, 512, BF16),
+                                                (65541, 256, BF16)])
 def test_greedy_lm_head_matches_unfused(rt, vocab, dim, w_dtype):
     """The LM head with the argmax folded into it gives the logits of
     ammon_gemv_rmsnorm bit for bit and the token of ammon_greedy_next on
