@@ -219,13 +219,23 @@ void CausalAttentionBlock::record(Scheme &s, TensorView x, const CausalAttention
                                 head, q, cache.key.data(), cache.value.data(),
                                 abi(cache.key.dtype()), seq, st, table);
   });
-  s.record("attn_partial", [=](ammon_stream stream) {
-    return ammon_attention_partial(rt, stream, q, q_heads, cache.key.data(), cache.value.data(),
-                                   abi(cache.key.dtype()), kv_heads, head, seq, st, split, partial);
-  });
-  s.record("attn_combine", [=](ammon_stream stream) {
-    return ammon_attention_combine(rt, stream, partial, q_heads, head, seq, st, split, xb);
-  });
+  if (ammon_attention_splits(seq, split) == 1) {
+    // one split covers the cache: pass 1 writes the output, no merge launch
+    s.record("attention", [=](ammon_stream stream) {
+      return ammon_attention_decode(rt, stream, q, q_heads, cache.key.data(), cache.value.data(),
+                                    abi(cache.key.dtype()), kv_heads, head, seq, st, split,
+                                    partial, partial_bytes, xb);
+    });
+  } else {
+    s.record("attn_partial", [=](ammon_stream stream) {
+      return ammon_attention_partial(rt, stream, q, q_heads, cache.key.data(), cache.value.data(),
+                                     abi(cache.key.dtype()), kv_heads, head, seq, st, split,
+                                     partial);
+    });
+    s.record("attn_combine", [=](ammon_stream stream) {
+      return ammon_attention_combine(rt, stream, partial, q_heads, head, seq, st, split, xb);
+    });
+  }
   s.record("wo_residual", [=](ammon_stream stream) {
     return ammon_gemv(rt, stream, w.output.data(), abi(w.output.dtype()), hidden, q_heads * head,
                       xb, (float *)x.data(), (const float *)x.data());

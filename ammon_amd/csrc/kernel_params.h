@@ -74,6 +74,8 @@ typedef struct {
   uint32_t limit;           /* positions at or past it (<= seq) are out of range:
                                NaN output, no partial (seq for decode; the
                                positions the grid and scratch cover for prefill) */
+  uint32_t single_out;      /* pass 1 with splits == 1 writes out (the merge's
+                               result) instead of the partial; no pass 2 */
 } ammon_k_attention;
 
 typedef struct {

@@ -23,7 +23,10 @@
     __shared__ float lds[att_lds_floats(GMAX, CH)];                             \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                \
     AttnPartial<KV, CH, GMAX, HEAD, EXACT> unit;                                \
-    if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);                \
+    if (unit.begin(p, blockIdx.x, blockIdx.y))                                  \
+      unit.run(p, lds);                                                         \
+    else                                                                        \
+      direct_out_nan(p, blockIdx.y);                                            \
   }
 
 #define ATT_PARTIAL_G(PREFIX, KV, CH)                  \
@@ -59,7 +62,10 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
     __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                    \
     AttnPartialMfma<GMAX, NBUF> unit;                                               \
-    if (unit.begin(p, blockIdx.x, blockIdx.y)) unit.run(p, lds);                    \
+    if (unit.begin(p, blockIdx.x, blockIdx.y))                                      \
+      unit.run(p, lds);                                                             \
+    else                                                                            \
+      direct_out_nan(p, blockIdx.y);                                                \
   }
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1, 2)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2, 2)

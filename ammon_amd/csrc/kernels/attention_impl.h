@@ -36,6 +36,23 @@ AMMON_DEV float group_sum(float v, uint32_t width) {
   return v;
 }
 
+// A decode with a single split needs no merge pass: the merge of one split
+// is out = acc * e^0 / (l * e^0) = acc / l exactly (the combine's fmaf(x, 1,
+// 0) and +0 leave x unchanged), so pass 1 writes out itself when the launch
+// asks for it (single_out).
+AMMON_DEV bool direct_out(const ammon_k_attention &p) {
+  return p.single_out && p.splits == 1 && p.out != nullptr;
+}
+
+// ... and for a position out of range (no unit runs), the merge's NaN output
+// for kv head g's query heads.
+AMMON_DEV void direct_out_nan(const ammon_k_attention &p, uint32_t g) {
+  if (!direct_out(p)) return;
+  const uint32_t gq = p.q_heads / p.kv_heads;
+  for (uint32_t i = threadIdx.x; i < gq * p.head; i += AMMON_WG)
+    st_out(p.out + (size_t)g * gq * p.head + i, __uint_as_float(0x7fc00000u));
+}
+
 // One workgroup = one (split, kv head).  The split's positions are processed
 // in chunks of ATT_ROUNDS rounds; a round is 4 waves x (64 / P2) positions,
 // P2 lanes per position (the power of two >= head / CH), so each group of P2
@@ -276,6 +293,10 @@ struct AttnPartial {
         const uint32_t t = ((s >> lg_pw) << 6) + ((s & (PW - 1)) << lg_p2) + sb;
         total += s_red[t][j * CH + c] * w;
         L += s_l[s][j] * w;
+      }
+      if (direct_out(p)) {  // the only split: the merge's result, total / L
+        st_out(p.out + (size_t)(g * G + j) * head + d, total / L);
+        continue;
       }
       float *o = p.partial + ((size_t)(g * G + j) * p.splits + split) * slot_w;
       st_out(o + d, total);
@@ -547,6 +568,10 @@ struct AttnPartialMfma {
       float total = 0.f;
 #pragma unroll
       for (uint32_t s = 0; s < 16; ++s) total += s_red[(s >> 2) * 64 + (s & 3) * 16 + sb][j * 8 + e];
+      if (direct_out(p)) {  // the only split: the merge's result, total / l
+        st_out(p.out + (size_t)(g * GMAX + j) * HEAD + d, total / s_ml[GMAX + j]);
+        continue;
+      }
       float *o = p.partial + ((size_t)(g * GMAX + j) * p.splits + split) * slot_w;
       st_out(o + d, total);
       if (d == 0) {

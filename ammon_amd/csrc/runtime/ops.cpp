@@ -376,12 +376,16 @@ ammon_status ammon_cache_store(ammon_runtime *rt, ammon_stream stream, const flo
 }
 
 // ---- attention ---------------------------------------------------------------------------
-ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, const float *q,
-                                     uint32_t q_heads, const void *k_cache, const void *v_cache,
-                                     ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head,
-                                     uint32_t seq, const ammon_decode_step *step,
-                                     uint32_t split_len, float *partial) {
-  REQUIRE_RT();
+}  // extern "C"
+
+namespace {
+// Pass 1; with `single_out` (a decode whose split covers the whole cache) it
+// writes the merged output itself and no pass 2 is needed.
+ammon_status attention_pass1(ammon_runtime *rt, ammon_stream stream, const float *q,
+                             uint32_t q_heads, const void *k_cache, const void *v_cache,
+                             ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head, uint32_t seq,
+                             const ammon_decode_step *step, uint32_t split_len, float *partial,
+                             float *single_out) {
   AMMON_CHECK(q && k_cache && v_cache && step && partial,
               "attention_partial: NULL q, cache, step or partial");
   AMMON_CHECK(valid_dtype(kv_dtype), "attention_partial: unknown kv dtype %d", (int)kv_dtype);
@@ -391,9 +395,23 @@ ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, con
   AMMON_CHECK(f, "attention_partial: head %u needs an even width above 64", head);
   VALIDATE_ONLY();
   const uint32_t splits = ammon_attention_splits(seq, split_len);
-  ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, nullptr,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0, seq};
+  ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, single_out,
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, seq,
+                         single_out ? 1u : 0u};
   return launch_att(rt, stream, f, splits, kv_heads, 1, p, "attention_partial");
+}
+}  // namespace
+
+extern "C" {
+
+ammon_status ammon_attention_partial(ammon_runtime *rt, ammon_stream stream, const float *q,
+                                     uint32_t q_heads, const void *k_cache, const void *v_cache,
+                                     ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head,
+                                     uint32_t seq, const ammon_decode_step *step,
+                                     uint32_t split_len, float *partial) {
+  REQUIRE_RT();
+  return attention_pass1(rt, stream, q, q_heads, k_cache, v_cache, kv_dtype, kv_heads, head, seq,
+                         step, split_len, partial, nullptr);
 }
 
 ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
@@ -439,6 +457,9 @@ ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, cons
                                split_len, out);
   if (st != AMMON_OK) return st;
   VALIDATE_ONLY();
+  if (ammon_attention_splits(seq, split_len) == 1)  // one launch: pass 1 writes out
+    return attention_pass1(rt, stream, q, q_heads, k_cache, v_cache, kv_dtype, kv_heads, head,
+                           seq, step, split_len, partial, out);
   st = ammon_attention_partial(rt, stream, q, q_heads, k_cache, v_cache, kv_dtype, kv_heads, head,
                                seq, step, split_len, partial);
   if (st != AMMON_OK) return st;

@@ -509,8 +509,14 @@ size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t s
 // pipelines two chunks of K and V (64 positions of a 128-wide bf16 head
 // each) through registers, so a workgroup overlaps its own loads and
 // arithmetic.  Splits stay between 16 and AMMON_ATTENTION_MAX_SPLIT
-// positions and the count under AMMON_ATTENTION_MAX_SPLITS.
+// positions and the count under AMMON_ATTENTION_MAX_SPLITS.  A cache of at
+// most kSingleSplitSeq positions takes one split: the decode is then one
+// launch (pass 1 writes the merged output), which at that size saves more
+// than the split-level parallelism costs (the 6-layer dim-288 fp32 decoder
+// at 256 positions: 7921 against 7056 tokens/s).
+static constexpr uint32_t kSingleSplitSeq = 256;
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq) {
+  if (seq >= 1 && seq <= kSingleSplitSeq) return seq;
   const uint32_t cus = rt ? (uint32_t)rt->info.compute_units : 256u;
   const uint64_t target_wgs = 2ull * (cus ? cus : 256u);
   uint32_t split = 16;

@@ -168,7 +168,8 @@ uint32_t ammon_attention_splits(uint32_t seq, uint32_t split_len);
 size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t seq,
                                      uint32_t split_len);
 /* Split length the library picks for a kv-head count and cache length so that
- * kv_heads * splits fills the device at full context. */
+ * kv_heads * splits fills the device at full context; a cache of at most 256
+ * positions gets one split (the decode attention is then one launch). */
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq);
 
 /* ---- kernels ------------------------------------------------------------- */
@@ -226,7 +227,10 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
                                      uint32_t seq, const ammon_decode_step *step,
                                      uint32_t split_len, float *out);
 /* Both passes (the reference's attn_partial + attn_combine pair,
- * src/blocks.rs:240-253). */
+ * src/blocks.rs:240-253).  When one split covers the cache
+ * (ammon_attention_splits(seq, split_len) == 1) it is one launch: pass 1
+ * writes out itself (the merge of a single split, bit for bit) and leaves
+ * the partial scratch unwritten. */
 ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, const float *q,
                                     uint32_t q_heads, const void *k_cache, const void *v_cache,
                                     ammon_dtype kv_dtype, uint32_t kv_heads, uint32_t head,

@@ -273,9 +273,45 @@ def test_split_attention_matches_reference(rt, q_heads, kv_heads, head, seq, pos
         want = cpu_attention_f64(qh, kh, vh, q_heads, kv_heads, head, pos)
         assert np.max(np.abs(got - want)) < 1e-4, (pos, split)
         assert rel_err(got, oracle.attention(qh, kh, vh, F32, pos)) <= RTOL, (pos, split)
+        if part.shape[1] == 1:
+            continue  # one split: pass 1 writes the output, no partial
         live = pos // split + 1
         assert np.all(np.isfinite(part[:, :live])), pos
         assert np.all(np.isnan(part[:, live:])), "a dead split was written"
+
+
+@pytest.mark.parametrize("kv_dtype,q_heads,kv_heads,head", [
+    (F32, 6, 6, 48), (F32, 8, 2, 64), (BF16, 32, 8, 128), (BF16, 8, 8, 128), (BF16, 16, 8, 128),
+    (BF16, 32, 4, 128), (F32, 32, 8, 128)])
+def test_single_split_decode_matches_two_launches(rt, kv_dtype, q_heads, kv_heads, head):
+    # A split covering the whole cache: ammon_attention_decode runs pass 1
+    # alone, which writes acc / l -- the merge of one split -- so the output
+    # equals the explicit partial + combine pair bit for bit, and a position
+    # past the cache gives the combine's NaN row.
+    seq = 256
+    qh = oracle.normal(q_heads * head, 151).reshape(q_heads, head)
+    kh = oracle.storage(oracle.normal(seq * kv_heads * head, 152), kv_dtype).reshape(
+        seq, kv_heads, head)
+    vh = oracle.storage(oracle.normal(seq * kv_heads * head, 153), kv_dtype).reshape(
+        seq, kv_heads, head)
+    q = up(rt, qh)
+    kc, vc = up(rt, head_major(kh, kv_heads, seq, head)), up(rt, head_major(vh, kv_heads, seq, head))
+    part = rt.alloc(q_heads * (head + 2) * 4)
+    one, two = rt.alloc(q_heads * head * 4), rt.alloc(q_heads * head * 4)
+    step = rt.step(0, 0)
+    for pos in (0, 1, 63, 64, 200, 255, 256):
+        rt.deposit(step, 0, pos)
+        call("ammon_attention_decode", rt.handle, None, q, q_heads, kc, vc, kv_dtype, kv_heads,
+             head, seq, step, seq, part, q_heads * (head + 2) * 4, one)
+        call("ammon_attention_partial", rt.handle, None, q, q_heads, kc, vc, kv_dtype, kv_heads,
+             head, seq, step, seq, part)
+        call("ammon_attention_combine", rt.handle, None, part, q_heads, head, seq, step, seq, two)
+        got, want = down(one, (q_heads, head)), down(two, (q_heads, head))
+        if pos >= seq:
+            assert np.all(np.isnan(got)) and np.all(np.isnan(want))
+            continue
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32), err_msg=str(pos))
+        assert rel_err(got, oracle.attention(qh, kh, vh, kv_dtype, pos)) <= RTOL, pos
 
 
 def test_attention_partials_match_oracle_split8(rt):

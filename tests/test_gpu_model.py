@@ -148,7 +148,8 @@ def test_llama3_8b_width_two_layers(rt, kv_dtype):
     want_toks, want_logits = oracle.Model(cfg, dict(weights)).generate_tokens(prompt, 9)
     np.testing.assert_array_equal(toks, want_toks)
     assert rel_err(logits, want_logits) <= tol(kv_dtype)
-    assert m.launches == 1 + 6 * cfg.n_layers + 1
+    # a 64-position cache takes one attention split: pass 1 writes the output
+    assert m.launches == 1 + 5 * cfg.n_layers + 1
     m.close()
 
 
