@@ -256,8 +256,9 @@ DOMINANT_NAME = "ammon_gemv_bf16_v_swiglu (gate/up GEMV + SwiGLU, RMSNorm prolog
 def prefill_measure(rt, model, c, prompt_lengths=(16, 512), reps=3):
     """Prompt prefill (one pass per layer: GEMMs on matrix cores, token-
     batched attention) of T-token prompts from position 0: whole-model
-    time, and the gate/up GEMM + SwiGLU alone (events around 10 launches on
-    the model's stream).  Short prompts are HBM-bound on W (bytes: W once +
+    time, and the gate/up GEMM + SwiGLU alone (events on the model's stream
+    around one launch per layer's weights, so no launch finds its 235 MB of
+    weights in the 256 MB MALL).  Short prompts are HBM-bound on W (bytes: W once +
     x + hb); long ones are matrix-core bound, the bf16 W against x split
     into three bf16 parts (three MFMAs per product: issued TFLOP/s = 3 x
     algorithmic)."""
@@ -281,13 +282,16 @@ def prefill_measure(rt, model, c, prompt_lengths=(16, 512), reps=3):
         x = rt.alloc(T * c.dim * 4)
         rt.fill_normal(x, F32, T * c.dim, 1, 7)
         hb = rt.alloc(T * c.hidden * 4)
-        args = (rt.handle, stream, x, T, w1, w3, BF16, c.dim, c.hidden, hb)
-        call("ammon_prefill_gate_up_swiglu", *args)
+        per = c.hidden * c.dim * 2  # bytes of one layer's w1 (and w3)
+        layer_args = [(rt.handle, stream, x, T, ctypes.c_void_p(w1.value + l * per),
+                       ctypes.c_void_p(w3.value + l * per), BF16, c.dim, c.hidden, hb)
+                      for l in range(c.n_layers)]
+        call("ammon_prefill_gate_up_swiglu", *layer_args[-1])
         timer.start(stream)
-        for _ in range(10):
+        for args in layer_args:
             call("ammon_prefill_gate_up_swiglu", *args)
         timer.stop(stream)
-        us = timer.elapsed_ms() * 1e3 / 10
+        us = timer.elapsed_ms() * 1e3 / len(layer_args)
         x.free()
         hb.free()
         nbytes = 2 * c.hidden * c.dim * 2 + T * c.dim * 4 + T * c.hidden * 4
