@@ -1,0 +1,71 @@
+"""The HIP model against an independent implementation: Hugging Face
+transformers' LlamaForCausalLM (CPU, fp32, random weights) converted as
+llama2.c's export.py converts Hugging Face checkpoints (tests/hf_reference.py).
+fp32 weights and cache: logits within 1e-5 at every prompt position and the
+greedy continuation identical (near-ties aside), built from the arrays and
+loaded from llama2.c files of both layouts; bf16 weights: logits within
+2e-2, the bf16-against-fp32-weights bar."""
+import numpy as np
+import pytest
+
+import oracle
+from ammon_amd import LlamaModel
+from ammon_amd._abi import BF16, F32
+from oracle import llama2c
+
+pytestmark = pytest.mark.gpu
+pytest.importorskip("transformers")
+import hf_reference as hf  # noqa: E402
+
+CFG = oracle.LlamaConfig(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden=520, vocab=611,
+                         max_seq=48, w_dtype=F32, kv_dtype=F32)
+PROMPT = [1, 610, 37, 37, 5, 200, 42, 7]
+
+
+def rel(got, want):
+    return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / np.max(np.abs(want)))
+
+
+@pytest.fixture(scope="module")
+def hf_case():
+    m = hf.hf_model(CFG, seed=3)
+    w = hf.to_arrays(m, CFG)
+    toks, margins = hf.greedy(m, PROMPT, 12)
+    return w, hf.logits(m, PROMPT), toks, margins
+
+
+@pytest.mark.parametrize("source", ["arrays", "file_v0", "file_v1"])
+def test_model_matches_hf_llama(rt, tmp_path, hf_case, source):
+    w, want, want_toks, margins = hf_case
+    if source == "arrays":
+        model = LlamaModel.from_host(rt, CFG, w)
+    else:
+        path = tmp_path / "hf.bin"
+        llama2c.write(path, CFG, w, version=0 if source == "file_v0" else 1, shared=False)
+        model = LlamaModel.from_checkpoint(rt, str(path), w_dtype=F32)
+    try:
+        got = None
+        for pos, tok in enumerate(PROMPT):
+            got = model.step(tok, pos)
+            assert rel(got, want[pos]) <= 1e-5, (source, pos)
+        tok = int(np.argmax(got))
+        for i, (wt, margin) in enumerate(zip(want_toks, margins)):
+            if margin < 1e-4:
+                break  # a near-tie: either token is the fp32 model's answer
+            assert tok == wt, (source, i)
+            got = model.step(tok, len(PROMPT) + i)
+            tok = int(np.argmax(got))
+    finally:
+        model.close()
+
+
+def test_bf16_model_within_bf16_bar_of_hf_llama(rt, hf_case):
+    w, want, _, _ = hf_case
+    cfg = oracle.LlamaConfig(**{**CFG.__dict__, "w_dtype": BF16, "kv_dtype": BF16})
+    wb = {k: (v if k.startswith("rms") else oracle.storage(v, BF16)) for k, v in w.items()}
+    model = LlamaModel.from_host(rt, cfg, wb)
+    try:
+        for pos, tok in enumerate(PROMPT):
+            assert rel(model.step(tok, pos), want[pos]) <= 2e-2, pos
+    finally:
+        model.close()
