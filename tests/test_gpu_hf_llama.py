@@ -17,8 +17,15 @@ pytestmark = pytest.mark.gpu
 pytest.importorskip("transformers")
 import hf_reference as hf  # noqa: E402
 
-CFG = oracle.LlamaConfig(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden=520, vocab=611,
-                         max_seq=48, w_dtype=F32, kv_dtype=F32)
+SHAPES = {
+    # head 64, GQA 2:1, RoPE base 1e4 (llama2.c-style)
+    "small": oracle.LlamaConfig(dim=256, n_layers=2, n_heads=4, n_kv_heads=2, hidden=520,
+                                vocab=611, max_seq=48, w_dtype=F32, kv_dtype=F32),
+    # Llama-3-style heads: 128 wide, GQA 4:1, RoPE base 5e5
+    "llama3": oracle.LlamaConfig(dim=1024, n_layers=2, n_heads=8, n_kv_heads=2, hidden=2816,
+                                 vocab=1000, max_seq=48, theta=500000.0, w_dtype=F32,
+                                 kv_dtype=F32),
+}
 PROMPT = [1, 610, 37, 37, 5, 200, 42, 7]
 
 
@@ -26,23 +33,25 @@ def rel(got, want):
     return float(np.max(np.abs(np.asarray(got, np.float64) - want)) / np.max(np.abs(want)))
 
 
-@pytest.fixture(scope="module")
-def hf_case():
-    m = hf.hf_model(CFG, seed=3)
-    w = hf.to_arrays(m, CFG)
+@pytest.fixture(scope="module", params=sorted(SHAPES))
+def hf_case(request):
+    cfg = SHAPES[request.param]
+    m = hf.hf_model(cfg, seed=3)
+    w = hf.to_arrays(m, cfg)
     toks, margins = hf.greedy(m, PROMPT, 12)
-    return w, hf.logits(m, PROMPT), toks, margins
+    return cfg, w, hf.logits(m, PROMPT), toks, margins
 
 
 @pytest.mark.parametrize("source", ["arrays", "file_v0", "file_v1"])
 def test_model_matches_hf_llama(rt, tmp_path, hf_case, source):
-    w, want, want_toks, margins = hf_case
+    CFG, w, want, want_toks, margins = hf_case
     if source == "arrays":
         model = LlamaModel.from_host(rt, CFG, w)
     else:
         path = tmp_path / "hf.bin"
         llama2c.write(path, CFG, w, version=0 if source == "file_v0" else 1, shared=False)
-        model = LlamaModel.from_checkpoint(rt, str(path), w_dtype=F32)
+        # the file carries no RoPE base: pass the model's
+        model = LlamaModel.from_checkpoint(rt, str(path), w_dtype=F32, theta=CFG.theta)
     try:
         got = None
         for pos, tok in enumerate(PROMPT):
@@ -60,7 +69,7 @@ def test_model_matches_hf_llama(rt, tmp_path, hf_case, source):
 
 
 def test_bf16_model_within_bf16_bar_of_hf_llama(rt, hf_case):
-    w, want, _, _ = hf_case
+    CFG, w, want, _, _ = hf_case
     cfg = oracle.LlamaConfig(**{**CFG.__dict__, "w_dtype": BF16, "kv_dtype": BF16})
     wb = {k: (v if k.startswith("rms") else oracle.storage(v, BF16)) for k, v in w.items()}
     model = LlamaModel.from_host(rt, cfg, wb)

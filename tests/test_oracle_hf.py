@@ -14,9 +14,11 @@ import oracle
 pytest.importorskip("transformers")
 import hf_reference as hf  # noqa: E402
 
-# (dim, layers, heads, kv heads, hidden, vocab): GQA 2:1 at head 64, and no
-# GQA at head 64 with odd widths elsewhere
-SHAPES = [(256, 2, 4, 2, 520, 611), (192, 2, 3, 3, 300, 257)]
+# (dim, layers, heads, kv heads, hidden, vocab, RoPE base): GQA 2:1 at head
+# 64, no GQA at head 64 with odd widths elsewhere, and Llama-3-style heads
+# (128 wide, GQA 4:1, base 5e5)
+SHAPES = [(256, 2, 4, 2, 520, 611, 10000.0), (192, 2, 3, 3, 300, 257, 10000.0),
+          (1024, 2, 8, 2, 2816, 1000, 500000.0)]
 
 
 def rel(got, want):
@@ -25,9 +27,9 @@ def rel(got, want):
 
 @pytest.mark.parametrize("shape", SHAPES)
 def test_oracle_model_matches_hf_llama(shape):
-    dim, layers, heads, kv_heads, hidden, vocab = shape
+    dim, layers, heads, kv_heads, hidden, vocab, theta = shape
     cfg = oracle.LlamaConfig(dim=dim, n_layers=layers, n_heads=heads, n_kv_heads=kv_heads,
-                             hidden=hidden, vocab=vocab, max_seq=48)
+                             hidden=hidden, vocab=vocab, max_seq=48, theta=theta)
     m = hf.hf_model(cfg, seed=3)
     om = oracle.Model(cfg, hf.to_arrays(m, cfg))
     try:
