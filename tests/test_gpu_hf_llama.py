@@ -78,3 +78,33 @@ def test_bf16_model_within_bf16_bar_of_hf_llama(rt, hf_case):
             assert rel(model.step(tok, pos), want[pos]) <= 2e-2, pos
     finally:
         model.close()
+
+
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+def test_long_prompt_prefill_and_decode_match_hf_llama(rt, kv_dtype):
+    # A 600-token prompt through the one-pass prefill (matrix-core GEMMs,
+    # token-batched split attention over several splits), then decode steps
+    # at positions 600..603, against the Hugging Face forward over the same
+    # tokens.  fp32 weights.  A bf16 cache rounds every stored K/V element
+    # against the reference's unrounded ones, so it gets the bf16 bar (2e-2,
+    # as bf16 weights against fp32; measured ~8e-3 here).
+    cfg = oracle.LlamaConfig(**{**SHAPES["llama3"].__dict__, "max_seq": 640,
+                                "kv_dtype": kv_dtype})
+    m = hf.hf_model(cfg, seed=5)
+    w = hf.to_arrays(m, cfg)
+    prompt = [int(t) for t in np.random.default_rng(7).integers(1, cfg.vocab, 600)]
+    model = LlamaModel.from_host(rt, cfg, w)
+    bar = 1e-5 if kv_dtype == F32 else 2e-2
+    try:
+        want = hf.logits(m, prompt)
+        got = model.prefill(prompt)
+        assert rel(got, want[-1]) <= bar
+        seq = list(prompt)
+        for pos in range(600, 604):
+            tok = int(np.argmax(want[-1]))
+            seq.append(tok)
+            want = hf.logits(m, seq)
+            got = model.step(tok, pos)
+            assert rel(got, want[-1]) <= bar, pos
+    finally:
+        model.close()
