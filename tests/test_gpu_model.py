@@ -14,7 +14,7 @@ import numpy as np
 import pytest
 
 import oracle
-from ammon_amd import AmmonError, LlamaModel
+from ammon_amd import AmmonError, LlamaModel, _abi
 from ammon_amd._abi import BF16, F32
 
 pytestmark = pytest.mark.gpu
@@ -28,16 +28,30 @@ def tol(kv_dtype):
     return RTOL if kv_dtype == F32 else BF16_KV_TOL
 
 
-def block_launches(cfg):
+def attention_launches(rt, cfg, split=0):
+    """The decode attention pair's launches: one where a single split covers
+    the cache (pass 1 writes the output), else two."""
+    split = split or int(_abi.lib.ammon_attention_default_split(rt.handle, cfg.n_kv_heads,
+                                                                cfg.max_seq))
+    return 1 if int(_abi.lib.ammon_attention_splits(cfg.max_seq, split)) == 1 else 2
+
+
+def layer_launches(rt, cfg, split=0):
+    """Launches one layer records: norm+QKV, attention, Wo, gate/up, W2."""
+    return 4 + attention_launches(rt, cfg, split)
+
+
+def block_launches(rt, cfg, split=0):
     """Launches one layer records with one_launch_blocks: one per attention
     / SwiGLU block where one launch applies (bf16 weights; the attention
     block also a bf16 KV cache, head 128 and 1-4 q heads per kv head), else
-    4 and 2."""
+    the separate launches."""
     head = cfg.dim // cfg.n_heads
     g = cfg.n_heads // cfg.n_kv_heads
     one_attn = cfg.w_dtype == BF16 and cfg.kv_dtype == BF16 and head == 128 and g in (1, 2, 4)
     one_ffn = cfg.w_dtype == BF16
-    return (1 if one_attn else 4) + (1 if one_ffn else 2)
+    attn = 1 if one_attn else 2 + attention_launches(rt, cfg, split)
+    return attn + (1 if one_ffn else 2)
 
 
 def rel_err(got, want):
@@ -148,8 +162,7 @@ def test_llama3_8b_width_two_layers(rt, kv_dtype):
     want_toks, want_logits = oracle.Model(cfg, dict(weights)).generate_tokens(prompt, 9)
     np.testing.assert_array_equal(toks, want_toks)
     assert rel_err(logits, want_logits) <= tol(kv_dtype)
-    # a 64-position cache takes one attention split: pass 1 writes the output
-    assert m.launches == 1 + 5 * cfg.n_layers + 1
+    assert m.launches == 1 + layer_launches(rt, cfg) * cfg.n_layers + 1
     m.close()
 
 
@@ -177,6 +190,28 @@ PERSISTENT_SHAPES = [  # (n_heads, n_kv_heads): q heads per kv head 4, 1, 2, 8
 
 
 @pytest.mark.parametrize("kv_dtype", [BF16, F32])
+def test_persistent_token_kernel_single_split_matches_launch_list(rt, kv_dtype):
+    # A 192-position cache takes the library's single split: the launch list
+    # runs pass 1 alone (acc / l), the persistent kernel its partial + merge
+    # phases -- bit-identical, as the merge of one split is acc / l exactly.
+    cfg = oracle.LlamaConfig(dim=4096, n_layers=2, n_heads=32, n_kv_heads=8, hidden=1544,
+                             vocab=5003, max_seq=192, theta=500000.0, w_dtype=BF16,
+                             kv_dtype=kv_dtype)
+    ref = LlamaModel.synthetic(rt, cfg, seed=35, std=0.05)
+    rt.synchronize()
+    fused = LlamaModel(rt, cfg, ref.weights, persistent=True)
+    assert fused.launches == 1
+    assert ref.launches == 1 + 5 * cfg.n_layers + 1
+    for pos, tok in enumerate([7, 4093, 12, 5002, 300, 1]):
+        np.testing.assert_array_equal(fused.step(tok, pos), ref.step(tok, pos))
+    got = fused.decode(11, cfg.max_seq - 8, 8, read_tokens=True)
+    want = ref.decode(11, cfg.max_seq - 8, 8, read_tokens=True)
+    np.testing.assert_array_equal(got, want)
+    fused.close()
+    ref.close()
+
+
+@pytest.mark.parametrize("kv_dtype", [BF16, F32])
 @pytest.mark.parametrize("heads", PERSISTENT_SHAPES)
 def test_persistent_token_kernel_matches_launch_list(rt, heads, kv_dtype):
     n_heads, n_kv = heads
@@ -190,7 +225,8 @@ def test_persistent_token_kernel_matches_launch_list(rt, heads, kv_dtype):
         rt.fill_normal(ref.weights[name], F32, n, 32, i, 1.0, 0.2)
     rt.synchronize()
     fused = LlamaModel(rt, cfg, ref.weights, persistent=True, split_len=32)
-    assert fused.launches == 1 and ref.launches == 1 + 6 * cfg.n_layers + 1
+    assert fused.launches == 1
+    assert ref.launches == 1 + layer_launches(rt, cfg, 32) * cfg.n_layers + 1
     prompt = [7, 4093, 12, 5002, 300, 1]
     for pos, tok in enumerate(prompt):
         np.testing.assert_array_equal(fused.step(tok, pos), ref.step(tok, pos))
@@ -266,6 +302,8 @@ ONE_LAUNCH_SHAPES = [  # (n_heads, n_kv_heads, kv dtype, max_seq, split)
     (32, 8, F32, 300, 32),     # fp32 cache: separate attention launches, one SwiGLU launch
     (32, 4, BF16, 300, 32),    # 8: separate attention launches
     (32, 8, BF16, 8192, 64),   # more attention units (1024) than workgroups
+    (32, 8, BF16, 200, 0),     # one split: the launch list's attention is one launch
+    (32, 8, F32, 200, 0),      # one split, fp32 cache: the same one launch on both sides
 ]
 
 
@@ -282,8 +320,8 @@ def test_one_launch_blocks_match_launch_list(rt, shape):
         rt.fill_normal(ref.weights[name], F32, n, 34, i, 1.0, 0.2)
     rt.synchronize()
     one = LlamaModel(rt, cfg, ref.weights, split_len=split, one_launch_blocks=True)
-    assert ref.launches == 1 + 6 * cfg.n_layers + 1
-    assert one.launches == 1 + block_launches(cfg) * cfg.n_layers + 1
+    assert ref.launches == 1 + layer_launches(rt, cfg, split) * cfg.n_layers + 1
+    assert one.launches == 1 + block_launches(rt, cfg, split) * cfg.n_layers + 1
     prompt = [7, 4093, 12, 5002, 300, 1]
     for pos, tok in enumerate(prompt):
         np.testing.assert_array_equal(one.step(tok, pos), ref.step(tok, pos))
