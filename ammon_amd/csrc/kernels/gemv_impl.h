@@ -187,8 +187,9 @@ struct GemvPass {
     // loop.
     constexpr int XREG = 4;
     const bool xvec = (n & 3u) == 0 && (((uintptr_t)p.x) & 15u) == 0;
-    const bool wvec = p.norm_w == nullptr || p.norm_dtype == AMMON_K_BF16 ||
-                      (((uintptr_t)p.norm_w) & 15u) == 0;
+    // norm weights read four at a time: 8-byte (bf16) or 16-byte (fp32) loads
+    const bool wvec = p.norm_w == nullptr ||
+                      (((uintptr_t)p.norm_w) & (p.norm_dtype == AMMON_K_BF16 ? 7u : 15u)) == 0;
     if (!p.norm_w && xvec && n / 4 > XREG * AMMON_WG) {
       // Long x without a norm (the down projection): 16-byte buffer loads
       // straight into LDS, all of a wave's in flight at once and no

@@ -465,6 +465,23 @@ def test_gemv_rmsnorm_prologue_matches_separate_norm(rt, n, g_dtype):
     assert rel_err(got, want) <= RTOL
 
 
+@pytest.mark.parametrize("n", [4096, 8192])
+def test_gemv_rmsnorm_unaligned_bf16_norm_weight(rt, n):
+    # A bf16 norm weight 2 bytes into its buffer takes the element-wise
+    # pass instead of 8-byte loads; the output is the same bit for bit.
+    d = 512
+    wh = oracle.storage(oracle.normal(d * n, 95, std=0.02), BF16).reshape(d, n)
+    xh = oracle.normal(n, 96) * 3
+    gh = oracle.storage(1.0 + 0.1 * oracle.normal(n, 97), BF16)
+    w, x = up(rt, wh), up(rt, xh)
+    g = up(rt, gh)
+    g_off = up(rt, np.concatenate([np.zeros(1, np.uint16), gh]))
+    y1, y2 = rt.alloc(d * 4), rt.alloc(d * 4)
+    call("ammon_gemv_rmsnorm", rt.handle, None, x, g, BF16, 1e-5, w, BF16, d, n, y1)
+    call("ammon_gemv_rmsnorm", rt.handle, None, x, g_off.offset(2), BF16, 1e-5, w, BF16, d, n, y2)
+    np.testing.assert_array_equal(down(y2, d).view(np.uint32), down(y1, d).view(np.uint32))
+
+
 def test_gemv_validation(rt):
     x = up(rt, np.zeros(8, np.float32))
     with pytest.raises(AmmonError, match="y overlaps x"):
