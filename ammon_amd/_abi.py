@@ -79,6 +79,7 @@ SIGNATURES = {
     "ammon_attention_splits": (_U32, [_U32, _U32]),
     "ammon_attention_scratch_bytes": (_SZ, [_U32, _U32, _U32, _U32]),
     "ammon_attention_default_split": (_U32, [_P, _U32, _U32]),
+    "ammon_attention_default_split_for": (_U32, [_P, _U32, _U32, _U32, _DT, _U32]),
     "ammon_embed": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _P]),
     "ammon_embed_rows": (_ST, [_P, _P, _P, _DT, _U32, _U32, _P, _U32, _P]),
     "ammon_rmsnorm": (_ST, [_P, _P, _P, _P, _DT, _P, _U32, _U32, _F]),

@@ -131,9 +131,11 @@ CausalAttentionBlock::CausalAttentionBlock(const Runtime &rt, uint32_t hidden, u
   need(head_ % 2 == 0, "attention: head size " + std::to_string(head_) + " must be even for RoPE");
   xb_ = Tensor::zeros(rt, Shape::from_dims({query_heads, head_}), DType::F32);
   q_ = Tensor::zeros(rt, Shape::from_dims({query_heads, head_}), DType::F32);
-  // Scratch for the most splits any kv-head count will use: the split
-  // length grows with kv_heads, so kv_heads = 1 bounds the count.
-  const uint32_t min_split = split_len_for(1);
+  // Scratch for the most splits any shape will use: the split length grows
+  // with kv_heads and with fewer units per CU, so kv_heads = 1 at two units
+  // per CU bounds the count.
+  const uint32_t min_split =
+      opts_.split_len ? opts_.split_len : ammon_attention_default_split(rt.raw(), 1, seq_len);
   max_splits_ = ammon_attention_splits(seq_len, min_split);
   partial_ = Tensor::zeros(rt, Shape::from_dims({query_heads, max_splits_, head_ + 2}), DType::F32);
   sync_ = Tensor::zeros(rt, Shape::vector(AMMON_BLOCK_SYNC_WORDS), DType::U32);
@@ -144,9 +146,10 @@ void CausalAttentionBlock::check(ammon_stream stream) const {
   ammon::check(ammon_block_sync_check(rt_.raw(), stream, (uint32_t *)sync_.data()), "attention");
 }
 
-uint32_t CausalAttentionBlock::split_len_for(uint32_t kv_heads) const {
+uint32_t CausalAttentionBlock::split_len_for(uint32_t kv_heads, DType kv_dtype) const {
   if (opts_.split_len) return opts_.split_len;
-  return ammon_attention_default_split(rt_.raw(), kv_heads, seq_);
+  return ammon_attention_default_split_for(rt_.raw(), q_heads_, kv_heads, head_,
+                                           (ammon_dtype)kv_dtype, seq_);
 }
 
 void CausalAttentionBlock::record(Scheme &s, TensorView x, const CausalAttentionBlockWeights &w,
@@ -183,7 +186,7 @@ void CausalAttentionBlock::record(Scheme &s, TensorView x, const CausalAttention
            ", " + std::to_string(head_) + "] (kv_heads, seq, head), got " + dims(cache.key));
   need(cache.key.dtype() == cache.value.dtype(), k + ": key and value caches differ in dtype");
   need(step.nbytes() >= sizeof(ammon_decode_step), k + ": parameter `step` is not a DecodeStep");
-  const uint32_t split = split_len_for(kv_heads);
+  const uint32_t split = split_len_for(kv_heads, cache.key.dtype());
   need(ammon_attention_splits(seq_, split) <= max_splits_, k + ": split scratch too small");
 
   ammon_runtime *rt = s.runtime().raw();

@@ -433,9 +433,26 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
-                         ammon_attention_splits(seq, split_len), 0, seq};
+                         ammon_attention_splits(seq, split_len), 0, seq, 0};
   return launch_att(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 8), 1, p,
                     "attention_combine");
+}
+
+uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
+                                           uint32_t kv_heads, uint32_t head,
+                                           ammon_dtype kv_dtype, uint32_t seq) {
+  // Two units per CU where two pass-1 workgroups of this shape's kernel fit
+  // on a CU; one where only one does (the 8:1 group at head 128: one round
+  // of 256 long units, not two rounds of short ones -- the 70B-shaped layer
+  // at 32768 positions: 0.635-0.636 against 0.639-0.642 ms per step)
+  uint32_t per_cu = 2;
+  if (rt && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 8 && head > 0 &&
+      head <= AMMON_ATTENTION_MAX_HEAD && valid_dtype(kv_dtype)) {
+    DeviceGuard guard(rt->device);
+    hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, nullptr, nullptr);
+    if (f) per_cu = std::min<uint32_t>(occupancy(rt, f, 0), 2);
+  }
+  return default_split(rt, kv_heads, seq, per_cu);
 }
 
 ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, const float *q,
@@ -500,7 +517,7 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
   // out-of-range treatment -- NaN output, no partial -- like one past seq
   const uint32_t splits = ammon_attention_splits(ctx, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, out,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx};
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx, 0};
   st = launch_att(rt, stream, f, splits, kv_heads, tokens, p, "attention_prefill");
   if (st != AMMON_OK) return st;
   return launch_att(rt, stream, rt->k.att_combine_waves, cdiv(q_heads, kWaves), 1, tokens, p,
@@ -1028,7 +1045,7 @@ ammon_status ammon_attention_block(ammon_runtime *rt, ammon_stream stream, float
   AMMON_CHECK(vec_qkv && vec_wo, "%s: rows must be whole 16-byte chunks", what);
   const uint32_t splits = ammon_attention_splits(seq, split_len);
   p.att = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, att,
-           q_heads, kv_heads, head, seq, split_len, splits, 0, seq};
+           q_heads, kv_heads, head, seq, split_len, splits, 0, seq, 0};
   p.sync = sync;
   p.spin_limit = block_spin_limit();
   VALIDATE_ONLY();

@@ -9,6 +9,7 @@
 // kernel once; later creates share it; the last release unloads it.
 #include <hip/hip_runtime_api.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -516,9 +517,20 @@ size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t s
 // at 256 positions: 7921 against 7056 tokens/s).
 static constexpr uint32_t kSingleSplitSeq = 256;
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq) {
+  return ammon_rt::default_split(rt, kv_heads, seq, 2);
+}
+
+}  // extern "C"
+
+namespace ammon_rt {
+
+// The shortest power-of-two split from 16 up whose kv_heads * splits units
+// fit in units_per_cu units per CU (and under the split-count limit).
+uint32_t default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq,
+                       uint32_t units_per_cu) {
   if (seq >= 1 && seq <= kSingleSplitSeq) return seq;
   const uint32_t cus = rt ? (uint32_t)rt->info.compute_units : 256u;
-  const uint64_t target_wgs = 2ull * (cus ? cus : 256u);
+  const uint64_t target_wgs = (uint64_t)std::max(units_per_cu, 1u) * (cus ? cus : 256u);
   uint32_t split = 16;
   while (split < AMMON_ATTENTION_MAX_SPLIT &&
          ((uint64_t)kv_heads * ammon_attention_splits(seq, split) > target_wgs ||
@@ -527,4 +539,4 @@ uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uin
   return split;
 }
 
-}  // extern "C"
+}  // namespace ammon_rt

@@ -746,6 +746,9 @@ def main():
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain streaming kernel of known size (ammon_add over "
                          "256 MiB operands), the calibration for HBM byte counters")
+    ap.add_argument("--config", choices=("c1", "c5"),
+                    help="run only that workload's line (no headline) and print it as JSON: "
+                         "for profiling one workload on its own")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}): the decode "
@@ -755,6 +758,13 @@ def main():
     import ammon_amd
     from ammon_amd import Runtime, Timer
     from ammon_amd._abi import BF16, call
+
+    if args.config:
+        rt = Runtime(0)
+        cb = 0.0 if args.no_cpu else args.cpu_budget
+        fn = {"c1": lambda: c1_decode(rt, cb), "c5": lambda: c5_layer(rt, min(cb, 10.0))}
+        print(json.dumps({"config": args.config, args.config: fn[args.config]()}), flush=True)
+        return
 
     c = Cfg(**LLAMA3_8B, w_dtype=BF16, kv_dtype=BF16)
     total = args.steps + args.warmup

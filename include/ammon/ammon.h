@@ -171,6 +171,13 @@ size_t ammon_attention_scratch_bytes(uint32_t q_heads, uint32_t head, uint32_t s
  * kv_heads * splits fills the device at full context; a cache of at most 256
  * positions gets one split (the decode attention is then one launch). */
 uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq);
+/* The same choice for a full attention shape, which the model uses: the
+ * unit count is sized to the pass-1 workgroups of that shape's kernel that
+ * fit on a CU (two, or one for a kernel that fits only once), so a kernel
+ * that runs one workgroup per CU gets one round of longer splits. */
+uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
+                                           uint32_t kv_heads, uint32_t head,
+                                           ammon_dtype kv_dtype, uint32_t seq);
 
 /* ---- kernels ------------------------------------------------------------- */
 

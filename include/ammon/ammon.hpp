@@ -341,7 +341,8 @@ class CausalAttentionBlock {
   void record_group(Scheme &s, const std::string &label, TensorView x,
                     const CausalAttentionBlockWeights &w, const KvLayer &cache,
                     const Tensor &step) const;
-  uint32_t split_len_for(uint32_t kv_heads) const;
+  // The split length record() uses for a cache of kv_heads heads in kv_dtype.
+  uint32_t split_len_for(uint32_t kv_heads, DType kv_dtype) const;
   // After the stream has drained: throws if a one-launch block recorded by
   // this module flagged a grid barrier that stopped waiting.
   void check(ammon_stream stream) const;

@@ -80,6 +80,11 @@ def test_attention_scratch_geometry():
     assert 16 <= split <= 1024 and split & (split - 1) == 0
     assert 8 * ammon_amd.attention_splits(8192, split) <= 2 * 256
     assert split == 128
+    # without a runtime there is no kernel to size for: two units per CU
+    for q_heads, kv_heads, seq in ((32, 8, 8192), (64, 8, 32768), (6, 6, 1000), (8, 8, 256)):
+        assert (_abi.lib.ammon_attention_default_split_for(None, q_heads, kv_heads, 128,
+                                                           _abi.BF16, seq)
+                == _abi.lib.ammon_attention_default_split(None, kv_heads, seq))
 
 
 def test_null_runtime_is_a_validation_error():

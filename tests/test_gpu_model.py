@@ -31,8 +31,9 @@ def tol(kv_dtype):
 def attention_launches(rt, cfg, split=0):
     """The decode attention pair's launches: one where a single split covers
     the cache (pass 1 writes the output), else two."""
-    split = split or int(_abi.lib.ammon_attention_default_split(rt.handle, cfg.n_kv_heads,
-                                                                cfg.max_seq))
+    split = split or int(_abi.lib.ammon_attention_default_split_for(
+        rt.handle, cfg.n_heads, cfg.n_kv_heads, cfg.dim // cfg.n_heads, cfg.kv_dtype,
+        cfg.max_seq))
     return 1 if int(_abi.lib.ammon_attention_splits(cfg.max_seq, split)) == 1 else 2
 
 
