@@ -55,7 +55,10 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 // group (the Llama-3 shape): at split 128 every workgroup requesting both of
 // its chunks at once delays all first chunks -- one buffer measured 0.1-0.7
 // us faster per launch at positions 1023..8191 (four buffers no faster than
-// two)
+// two).  One for the 8:1 group too: 242 VGPRs fit two workgroups per CU,
+// where two buffers (256 VGPRs + 70 AGPRs) fit one, and the Llama-3-70B
+// layer at 32768 positions then steps in 0.623-0.625 ms against 0.635-0.636
+// (each at its best split: 512 against 1024)
 #define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
   ATT_KERNEL(NAME) {                                                                \
     ATT_PARAMS(p0);                                                                 \
@@ -70,7 +73,7 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1, 2)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2, 2)
 ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4, 1)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 2)
+ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 1)
 ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 

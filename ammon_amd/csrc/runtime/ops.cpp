@@ -442,9 +442,11 @@ uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
                                            uint32_t kv_heads, uint32_t head,
                                            ammon_dtype kv_dtype, uint32_t seq) {
   // Two units per CU where two pass-1 workgroups of this shape's kernel fit
-  // on a CU; one where only one does (the 8:1 group at head 128: one round
-  // of 256 long units, not two rounds of short ones -- the 70B-shaped layer
-  // at 32768 positions: 0.635-0.636 against 0.639-0.642 ms per step)
+  // on a CU; one where only one does (the generic bf16 kernel of an 8:1
+  // group): one round of long units, not two rounds of short ones.  A
+  // two-buffer head-128 8:1 kernel that fit once per CU measured it on the
+  // 70B-shaped layer at 32768 positions: 0.635-0.636 against 0.639-0.642 ms
+  // per step.
   uint32_t per_cu = 2;
   if (rt && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 8 && head > 0 &&
       head <= AMMON_ATTENTION_MAX_HEAD && valid_dtype(kv_dtype)) {

@@ -327,17 +327,19 @@ def test_attention_partials_match_oracle_split8(rt):
 
 def test_default_split_sizes_units_to_kernel_occupancy(rt):
     """The model's split: two pass-1 units per CU where two of the shape's
-    workgroups fit on a CU, one where only one does (the 8:1 group at head
-    128 runs one workgroup per CU: one round of longer splits)."""
+    workgroups fit on a CU, one where only one does (the generic bf16
+    kernel of an 8:1 group runs one workgroup per CU: one round of longer
+    splits; the head-128 kernels fit two)."""
     lib = _abi.lib
     cus = rt.info.compute_units
     units = lambda kv_heads, seq, split: kv_heads * int(lib.ammon_attention_splits(seq, split))
-    # 4:1 at head 128, two per CU: the kv-head-count choice (512 units at 8k)
-    s = lib.ammon_attention_default_split_for(rt.handle, 32, 8, 128, BF16, 8192)
-    assert s == lib.ammon_attention_default_split(rt.handle, 8, 8192)
-    assert units(8, 8192, s) <= 2 * cus < units(8, 8192, s // 2)
-    # 8:1 at head 128, one per CU: the shortest split with at most one unit per CU
-    s = lib.ammon_attention_default_split_for(rt.handle, 64, 8, 128, BF16, 32768)
+    # 4:1 and 8:1 at head 128, two per CU: the kv-head-count choice
+    for q_heads, seq in ((32, 8192), (64, 32768)):
+        s = lib.ammon_attention_default_split_for(rt.handle, q_heads, 8, 128, BF16, seq)
+        assert s == lib.ammon_attention_default_split(rt.handle, 8, seq)
+        assert units(8, seq, s) <= 2 * cus < units(8, seq, s // 2)
+    # 8:1 at head 64 (the generic kernel), one per CU: at most one unit per CU
+    s = lib.ammon_attention_default_split_for(rt.handle, 64, 8, 64, BF16, 32768)
     assert units(8, 32768, s) <= cus < units(8, 32768, s // 2)
     # a cache of at most 256 positions: one split, whatever the shape
     assert lib.ammon_attention_default_split_for(rt.handle, 64, 8, 128, BF16, 256) == 256
