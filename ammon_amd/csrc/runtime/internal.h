@@ -78,9 +78,10 @@ constexpr uint32_t kWaves = kWorkgroup / 64;
 // dynamic LDS (hipModuleOccupancyMaxActiveBlocksPerMultiprocessor, cached).
 uint32_t occupancy(ammon_runtime *rt, hipFunction_t f, size_t shmem);
 // Attention split length for about units_per_cu pass-1 units per CU at the
-// cache length (one split for caches of at most 256 positions).
+// cache length, at least min_split (one split for caches of at most 256
+// positions).
 uint32_t default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq,
-                       uint32_t units_per_cu);
+                       uint32_t units_per_cu, uint32_t min_split = 16);
 
 // Makes `device` current for the scope's lifetime.
 struct DeviceScope {

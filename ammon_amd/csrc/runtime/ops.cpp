@@ -447,14 +447,22 @@ uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
   // two-buffer head-128 8:1 kernel that fit once per CU measured it on the
   // 70B-shaped layer at 32768 positions: 0.635-0.636 against 0.639-0.642 ms
   // per step.
-  uint32_t per_cu = 2;
+  //
+  // The matrix-core kernels (bf16 cache, head 128, power-of-two group)
+  // score 64-position chunks, so a split never goes below one chunk: a
+  // shorter one leaves most of each workgroup's chunk past its split
+  // (32 q / 8 kv heads, 1024 positions: 8.6 us at split 64 against 10.0 at
+  // 16; 2048: 9.7 against 10.6 at 32).
+  uint32_t per_cu = 2, min_split = 16;
   if (rt && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 8 && head > 0 &&
       head <= AMMON_ATTENTION_MAX_HEAD && valid_dtype(kv_dtype)) {
     DeviceGuard guard(rt->device);
     hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, nullptr, nullptr);
     if (f) per_cu = std::min<uint32_t>(occupancy(rt, f, 0), 2);
+    const uint32_t g = q_heads / kv_heads;
+    if (kv_dtype == AMMON_BF16 && head == 128 && (g & (g - 1)) == 0) min_split = 64;
   }
-  return default_split(rt, kv_heads, seq, per_cu);
+  return default_split(rt, kv_heads, seq, per_cu, min_split);
 }
 
 ammon_status ammon_attention_decode(ammon_runtime *rt, ammon_stream stream, const float *q,

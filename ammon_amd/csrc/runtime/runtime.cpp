@@ -524,14 +524,15 @@ uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uin
 
 namespace ammon_rt {
 
-// The shortest power-of-two split from 16 up whose kv_heads * splits units
-// fit in units_per_cu units per CU (and under the split-count limit).
+// The shortest power-of-two split from min_split (a power of two) up whose
+// kv_heads * splits units fit in units_per_cu units per CU (and under the
+// split-count limit).
 uint32_t default_split(ammon_runtime *rt, uint32_t kv_heads, uint32_t seq,
-                       uint32_t units_per_cu) {
+                       uint32_t units_per_cu, uint32_t min_split) {
   if (seq >= 1 && seq <= kSingleSplitSeq) return seq;
   const uint32_t cus = rt ? (uint32_t)rt->info.compute_units : 256u;
   const uint64_t target_wgs = (uint64_t)std::max(units_per_cu, 1u) * (cus ? cus : 256u);
-  uint32_t split = 16;
+  uint32_t split = std::min<uint32_t>(std::max<uint32_t>(min_split, 1), AMMON_ATTENTION_MAX_SPLIT);
   while (split < AMMON_ATTENTION_MAX_SPLIT &&
          ((uint64_t)kv_heads * ammon_attention_splits(seq, split) > target_wgs ||
           ammon_attention_splits(seq, split) > AMMON_ATTENTION_MAX_SPLITS))

@@ -93,7 +93,8 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
     step = rt.step(1, ctx - 1)
     table = rt.upload(ammon_amd.rope_table_host(c.theta, head, c.max_seq))
     if not split:
-        split = int(ammon_amd._abi.lib.ammon_attention_default_split(rt.handle, c.n_kv_heads, c.max_seq))
+        split = int(ammon_amd._abi.lib.ammon_attention_default_split_for(
+            rt.handle, c.n_heads, c.n_kv_heads, head, c.kv_dtype, c.max_seq))
     part_bytes = ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split)
     part = rt.alloc(part_bytes)
     att = rt.alloc(q * 4)
@@ -465,7 +466,8 @@ def c3_attention(rt, stream, cpu_budget):
     rt.synchronize()
     lines = {}
     for ctx in C3_CTX:
-        split = int(lib.ammon_attention_default_split(rt.handle, kv_heads, ctx))
+        split = int(lib.ammon_attention_default_split_for(rt.handle, q_heads, kv_heads, head, BF16,
+                                                          ctx))
         part_bytes = attention_scratch_bytes(q_heads, head, ctx, split)
         part = rt.alloc(part_bytes)
         per = kv_heads * ctx * head  # elements of one K (or V) cache

@@ -174,7 +174,9 @@ uint32_t ammon_attention_default_split(ammon_runtime *rt, uint32_t kv_heads, uin
 /* The same choice for a full attention shape, which the model uses: the
  * unit count is sized to the pass-1 workgroups of that shape's kernel that
  * fit on a CU (two, or one for a kernel that fits only once), so a kernel
- * that runs one workgroup per CU gets one round of longer splits. */
+ * that runs one workgroup per CU gets one round of longer splits; and the
+ * matrix-core kernels (bf16 cache, head 128, power-of-two group), which
+ * score 64-position chunks, get splits of at least 64. */
 uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
                                            uint32_t kv_heads, uint32_t head,
                                            ammon_dtype kv_dtype, uint32_t seq);

@@ -341,6 +341,12 @@ def test_default_split_sizes_units_to_kernel_occupancy(rt):
     # 8:1 at head 64 (the generic kernel), one per CU: at most one unit per CU
     s = lib.ammon_attention_default_split_for(rt.handle, 64, 8, 64, BF16, 32768)
     assert units(8, 32768, s) <= cus < units(8, 32768, s // 2)
+    # the matrix-core kernels score 64-position chunks: no split below 64,
+    # where the VALU kernels (fp32 cache) keep the unit-count choice
+    for seq in (1024, 2048):
+        assert lib.ammon_attention_default_split_for(rt.handle, 32, 8, 128, BF16, seq) == 64
+        assert (lib.ammon_attention_default_split_for(rt.handle, 32, 8, 128, F32, seq)
+                == lib.ammon_attention_default_split(rt.handle, 8, seq))
     # a cache of at most 256 positions: one split, whatever the shape
     assert lib.ammon_attention_default_split_for(rt.handle, 64, 8, 128, BF16, 256) == 256
 
