@@ -101,11 +101,6 @@ SIGNATURES = {
     "ammon_qkv_rope_store": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _P, _DT, _U32, _U32, _U32,
                                    _U32, _P, _P, _P, _DT, _U32, _P, _P]),
     "ammon_gate_up_swiglu": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _DT, _U32, _U32, _P]),
-    "ammon_attention_block": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _P, _P, _DT, _U32, _U32,
-                                    _U32, _U32, _P, _P, _DT, _U32, _P, _P, _U32, _P, _P, _P, _SZ,
-                                    _P]),
-    "ammon_swiglu_block": (_ST, [_P, _P, _P, _P, _DT, _F, _P, _P, _P, _DT, _U32, _U32, _P, _P]),
-    "ammon_block_sync_check": (_ST, [_P, _P, _P]),
     "ammon_argmax_scratch_bytes": (_SZ, [_U32]),
     "ammon_argmax": (_ST, [_P, _P, _P, _U32, _P, _P]),
     "ammon_greedy_next": (_ST, [_P, _P, _P, _U32, _P, _P, _U32, _P, _P, _U32]),
@@ -131,8 +126,7 @@ class LlamaConfig(ctypes.Structure):
     _fields_ = [("dim", _U32), ("n_layers", _U32), ("n_heads", _U32), ("n_kv_heads", _U32),
                 ("hidden", _U32), ("vocab", _U32), ("max_seq", _U32), ("theta", _F),
                 ("eps", _F), ("w_dtype", ctypes.c_int), ("kv_dtype", ctypes.c_int),
-                ("use_graph", _U32), ("split_len", _U32),
-                ("persistent", _U32), ("one_launch_blocks", _U32)]
+                ("use_graph", _U32), ("split_len", _U32)]
 
 
 class LlamaWeights(ctypes.Structure):
@@ -162,7 +156,6 @@ SIGNATURES.update({
     "ammon_llama_stream": (_ST, [_P, ctypes.POINTER(_P)]),
     "ammon_llama_logits": (_ST, [_P, ctypes.POINTER(_P)]),
     "ammon_llama_launches": (_ST, [_P, ctypes.POINTER(_U32)]),
-    "ammon_llama_token_trace": (_ST, [_P, _P, _SZ, ctypes.POINTER(_U32), ctypes.POINTER(_U32)]),
 })
 
 # include/ammon/ammon_checkpoint.h

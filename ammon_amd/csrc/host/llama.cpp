@@ -25,190 +25,6 @@ namespace ammon {
 const BpeTokenizer &bpe_of(const ammon_bpe *t);  // host/tokenizer.cpp
 namespace {
 
-// One cooperative launch per token (kernels/token.hip): the same arithmetic
-// as the launch list, with grid barriers instead of kernel boundaries.
-class PersistentToken {
- public:
-  // bf16 weights, head 128, 16-byte-aligned rows, 1/2/4/8 q heads per kv head.
-  static bool supported(const ammon_llama_config &c, uint32_t head) {
-    const uint32_t g = c.n_kv_heads ? c.n_heads / c.n_kv_heads : 0;
-    return c.w_dtype == AMMON_BF16 && head == 128 && (g == 1 || g == 2 || g == 4 || g == 8) &&
-           c.dim % 8 == 0 && c.hidden % 8 == 0 && (c.kv_dtype == AMMON_BF16 || c.kv_dtype == AMMON_F32);
-  }
-
-  PersistentToken(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w,
-                  const KvCache &cache, uint32_t requested_split, const Tensor &logits,
-                  const Tensor &step, const Tensor &prompt, const Tensor &tokens, const float *table)
-      : rt_(rt) {
-    ammon_runtime *raw = rt.raw();
-    const uint32_t head = c.dim / c.n_heads, g = c.n_heads / c.n_kv_heads;
-    const int gi = g == 1 ? 0 : g == 2 ? 1 : g == 4 ? 2 : 3;
-    const int di = c.kv_dtype == AMMON_BF16 ? 1 : 0;
-    f_ = raw->k.token[di][gi];
-    if (!f_) throw Error(AMMON_E_HIP, "persistent token kernel not loaded");
-    const uint32_t q_dim = c.n_heads * head;
-    // dynamic LDS: x staged for the widest GEMV input, or an attention /
-    // combine / argmax unit, whichever is larger
-    const uint32_t tile = 64 * AMMON_TOKEN_GEMV_U * 8;
-    auto padded = [&](uint32_t n) { return (n + tile - 1) / tile * tile; };
-    const uint32_t xs = std::max(std::max(padded(c.dim), padded(c.hidden)), padded(q_dim));
-    const uint32_t ach = c.kv_dtype == AMMON_BF16 ? 8 : 4;
-    const uint32_t att = 256 * (g * ach + 1) + 2 * 128 * g;
-    const uint32_t comb = 64 * 33 + 64 + 4;
-    shmem_ = 4 * std::max(std::max(xs, att), std::max(comb, 512u));
-    const uint32_t occ = ammon_rt::occupancy(raw, f_, shmem_);
-    if (occ == 0) throw Error(AMMON_E_HIP, "persistent token kernel does not fit on a CU");
-    grid_ = (uint32_t)raw->info.compute_units * std::min(occ, 2u);
-    // attention split: the caller's, else the shortest power of two (>= 16)
-    // whose (kv head, split) units fit the grid once -- each workgroup then
-    // streams one split, four 64-position chunks in flight
-    uint32_t split_len = requested_split;
-    if (!split_len) {
-      split_len = 16;
-      while (split_len < AMMON_ATTENTION_MAX_SPLIT &&
-             ((uint64_t)c.n_kv_heads * ammon_attention_splits(c.max_seq, split_len) > grid_ ||
-              ammon_attention_splits(c.max_seq, split_len) > AMMON_ATTENTION_MAX_SPLITS))
-        split_len *= 2;
-    }
-    const uint32_t splits = ammon_attention_splits(c.max_seq, split_len);
-
-    // one slice per phase and layer, each a whole number of 256-byte lines
-    auto line = [](uint64_t floats) { return (uint32_t)((floats + 63) / 64 * 64); };
-    const uint32_t L = c.n_layers;
-    const uint32_t xs_stride = line(c.dim), q_stride = line(q_dim), hb_stride = line(c.hidden);
-    const uint32_t part_stride =
-        line(ammon_attention_scratch_bytes(c.n_heads, head, c.max_seq, split_len) / 4);
-    x_ = Tensor::zeros(rt, Shape::vector((2 * L + 1) * xs_stride), DType::F32);
-    q_ = Tensor::zeros(rt, Shape::vector(L * q_stride), DType::F32);
-    att_ = Tensor::zeros(rt, Shape::vector(L * q_stride), DType::F32);
-    hb_ = Tensor::zeros(rt, Shape::vector(L * hb_stride), DType::F32);
-    partial_ = Tensor::zeros(rt, Shape::vector(L * part_stride), DType::F32);
-    cand_v_ = Tensor::zeros(rt, Shape::vector(grid_), DType::F32);
-    cand_i_ = Tensor::zeros(rt, Shape::vector(grid_), DType::U32);
-    sync_ = Tensor::zeros(rt, Shape::vector(AMMON_TOKEN_SYNC_WORDS), DType::U32);
-
-    ammon_k_token &p = p_;
-    p = ammon_k_token{};
-    p.tok_emb = w.tok_emb;
-    p.rms_att = w.rms_att;
-    p.rms_ffn = w.rms_ffn;
-    p.wq = w.wq;
-    p.wk = w.wk;
-    p.wv = w.wv;
-    p.wo = w.wo;
-    p.w1 = w.w1;
-    p.w3 = w.w3;
-    p.w2 = w.w2;
-    p.rms_final = w.rms_final;
-    p.wcls = w.wcls;
-    p.k_cache = cache.layer(0).key.data();
-    p.v_cache = cache.layer(0).value.data();
-    p.table = table;
-    p.step = (ammon_k_step *)step.data();
-    p.x = (float *)x_.data();
-    p.x_stride = xs_stride;
-    p.q_stride = q_stride;
-    p.hb_stride = hb_stride;
-    p.partial_stride = part_stride;
-    p.q = (float *)q_.data();
-    p.att = (float *)att_.data();
-    p.hb = (float *)hb_.data();
-    p.partial = (float *)partial_.data();
-    p.logits = (float *)logits.data();
-    p.cand_v = (float *)cand_v_.data();
-    p.cand_i = (uint32_t *)cand_i_.data();
-    p.sync = (uint32_t *)sync_.data();
-    p.dim = c.dim;
-    p.n_layers = c.n_layers;
-    p.q_heads = c.n_heads;
-    p.kv_heads = c.n_kv_heads;
-    p.head = head;
-    p.hidden = c.hidden;
-    p.vocab = c.vocab;
-    p.seq = c.max_seq;
-    p.split_len = split_len;
-    p.splits = splits;
-    p.eps = c.eps;
-    // a barrier polls about once per microsecond: give up after ~0.2 s.
-    // AMMON_TOKEN_SPIN_LIMIT overrides it (a tiny limit lets tests exercise
-    // the timeout report without anything hanging).
-    p.spin_limit = 200000;
-    if (const char *env = std::getenv("AMMON_TOKEN_SPIN_LIMIT")) {
-      const long v = std::atol(env);
-      if (v > 0) p.spin_limit = (uint32_t)std::min<long>(v, 200000);
-    }
-    prompt_ = (const int32_t *)prompt.data();
-    tokens_ = (int32_t *)tokens.data();
-    max_tokens_ = c.max_seq;
-    // AMMON_TOKEN_TRACE=1: stamp every barrier (embed, 6 per layer, LM head,
-    // argmax) of each launch; token_trace() reads the latest launch's stamps
-    if (const char *env = std::getenv("AMMON_TOKEN_TRACE"); env && std::atoi(env) > 0) {
-      p.trace_slots = 6 * L + 3;
-      trace_ = Tensor::zeros(rt, Shape::vector((size_t)4 * p.trace_slots * grid_), DType::U32);
-      p.trace = (uint64_t *)trace_.data();
-    }
-  }
-
-  // Enqueue one token on `s`.  greedy: argmax + prompt forcing + DecodeStep
-  // update on the device (n_prompt forced tokens from the prompt buffer).
-  void launch(ammon_stream s, bool greedy, uint32_t n_prompt) {
-    ammon_k_token p = p_;
-    p.greedy = greedy ? 1u : 0u;
-    p.prompt = greedy && n_prompt ? prompt_ : nullptr;
-    p.n_prompt = greedy ? n_prompt : 0u;
-    p.tokens = greedy ? tokens_ : nullptr;
-    p.max_tokens = max_tokens_;
-    void *args[] = {&p};
-    ammon_rt::DeviceScope scope(rt_.raw()->device);
-    const hipError_t e = hipModuleLaunchCooperativeKernel(
-        f_, grid_, 1, 1, ammon_rt::kWorkgroup, 1, 1, shmem_,
-        s ? (hipStream_t)s : rt_.raw()->stream, args);
-    if (e != hipSuccess)
-      throw Error(AMMON_E_HIP, std::string("persistent token launch: ") + hipGetErrorString(e));
-  }
-
-  // After the stream has drained: fail if a grid barrier timed out.
-  void check(ammon_stream s) const {
-    uint32_t err = 0;
-    ammon::check(ammon_memcpy(rt_.raw(), &err, (const uint32_t *)sync_.data() + AMMON_TOKEN_SYNC_ERR,
-                              sizeof err, AMMON_COPY_D2H, s),
-                 "persistent token");
-    ammon::check(ammon_stream_synchronize(rt_.raw(), s), "persistent token");
-    if (err) {
-      // results of that launch are invalid; clear the counters for the next
-      ammon::check(ammon_fill(rt_.raw(), s, sync_.data(), AMMON_F32, AMMON_TOKEN_SYNC_WORDS, 0.f),
-                   "persistent token");
-      ammon::check(ammon_stream_synchronize(rt_.raw(), s), "persistent token");
-      throw Error(AMMON_E_HIP,
-                  "persistent token kernel: a grid barrier timed out (workgroups not co-resident)");
-    }
-  }
-
-  uint32_t grid() const { return grid_; }
-
-  // Barrier stamps of the latest launch (after the stream has drained):
-  // copies up to `capacity` words; slots = 0 when tracing is off.
-  void token_trace(ammon_stream s, uint64_t *host, size_t capacity, uint32_t *slots,
-                   uint32_t *workgroups) const {
-    *slots = p_.trace_slots;
-    *workgroups = grid_;
-    const size_t words = std::min(capacity, (size_t)2 * p_.trace_slots * grid_);
-    if (!p_.trace || !words) return;
-    ammon::check(ammon_memcpy(rt_.raw(), host, p_.trace, words * 8, AMMON_COPY_D2H, s),
-                 "token trace");
-    ammon::check(ammon_stream_synchronize(rt_.raw(), s), "token trace");
-  }
-
- private:
-  Runtime rt_;
-  hipFunction_t f_ = nullptr;
-  uint32_t grid_ = 0, shmem_ = 0, max_tokens_ = 0;
-  ammon_k_token p_ = {};
-  const int32_t *prompt_ = nullptr;
-  int32_t *tokens_ = nullptr;
-  Tensor x_, q_, att_, hb_, partial_, cand_v_, cand_i_, sync_, trace_;
-};
-
 class LlamaModel : public AutoregressiveModel {
  public:
   LlamaModel(const Runtime &rt, const ammon_llama_config &c, const ammon_llama_weights &w);
@@ -228,14 +44,7 @@ class LlamaModel : public AutoregressiveModel {
   void read_tokens(uint32_t start, uint32_t n, int32_t *out);
   ammon_stream stream() const { return stream_; }
   float *device_logits() const { return (float *)logits_.data(); }
-  uint32_t launches() const {
-    return persistent_ ? 1u : (uint32_t)token_scheme_->ir_node_count();
-  }
-  void token_trace(uint64_t *host, size_t capacity, uint32_t *slots, uint32_t *workgroups) const {
-    *slots = 0;
-    *workgroups = 0;
-    if (persistent_) persistent_->token_trace(stream_, host, capacity, slots, workgroups);
-  }
+  uint32_t launches() const { return (uint32_t)token_scheme_->ir_node_count(); }
   // Host logits of the most recent step() (what generate_tokens last saw).
   const std::vector<float> &last_logits() const { return host_logits_; }
 
@@ -247,14 +56,6 @@ class LlamaModel : public AutoregressiveModel {
   void ensure_prefill(uint32_t n);
   const float *rope_table();
   void deposit(uint32_t token, uint32_t pos, ammon_stream stream);
-  // After `stream` has drained (it waits for it): throws if a one-launch
-  // block or the persistent kernel flagged a grid barrier that stopped
-  // waiting (that launch's results are invalid).
-  void check_blocks(ammon_stream stream) const {
-    if (persistent_) persistent_->check(stream);
-    attn_.check(stream);
-    ffn_.check(stream);
-  }
 
   Runtime rt_;
   ammon_llama_config c_;
@@ -270,7 +71,6 @@ class LlamaModel : public AutoregressiveModel {
   Tensor x_, logits_, step_, prompt_, tokens_, scratch_;
   ammon_stream stream_ = nullptr;  // both schemes replay here, in order
   std::unique_ptr<Scheme> token_scheme_, decode_scheme_;
-  std::unique_ptr<PersistentToken> persistent_;
   Tensor rope_table_;
   uint32_t decode_prompt_ = 0xffffffffu;
   ammon_decode_step *pinned_step_ = nullptr;
@@ -293,7 +93,6 @@ AttentionOptions attention_options(const ammon_llama_config &c) {
   o.theta = c.theta;
   o.eps = c.eps;
   o.split_len = c.split_len;
-  o.one_launch = c.one_launch_blocks != 0;
   return o;
 }
 
@@ -315,7 +114,7 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
       kv_dim_(head_ * c.n_kv_heads),
       embed_(rt),
       attn_(rt, c.dim, c.n_heads, c.max_seq, attention_options(c)),
-      ffn_(rt, c.dim, c.hidden, c.eps, c.one_launch_blocks != 0),
+      ffn_(rt, c.dim, c.hidden, c.eps),
       lm_head_(rt),
       cache_(rt, c.n_layers, c.max_seq, c.n_kv_heads, head_, dt(c.kv_dtype)) {
   const DType wd = dt(c.w_dtype);
@@ -350,14 +149,6 @@ LlamaModel::LlamaModel(const Runtime &rt, const ammon_llama_config &c, const amm
   check(ammon_stream_create(rt.raw(), &stream_), "llama stream");
   token_scheme_ = std::make_unique<Scheme>(rt, c.use_graph != 0, stream_);
   record_token(*token_scheme_);
-  if (c.persistent && PersistentToken::supported(c, head_)) {
-    std::vector<float> table(ammon_rope_table_bytes(head_, c.max_seq) / sizeof(float));
-    check(ammon_rope_table_host(c.theta, head_, c.max_seq, table.data()), "rope table");
-    rope_table_ = Tensor::from_f32(rt, Shape::vector((uint32_t)table.size()), table);
-    persistent_ = std::make_unique<PersistentToken>(
-        rt, c, w, cache_, c.split_len, logits_, step_, prompt_, tokens_,
-        (const float *)rope_table_.data());
-  }
 }
 
 LlamaModel::~LlamaModel() {
@@ -410,15 +201,11 @@ const std::vector<float> &LlamaModel::step(uint32_t token, uint32_t pos) {
     throw Error(AMMON_E_VALIDATION, "step: position " + std::to_string(pos) + " >= max_seq " +
                                         std::to_string(c_.max_seq));
   deposit(token, pos, stream_);
-  if (persistent_)
-    persistent_->launch(stream_, false, 0);
-  else
-    token_scheme_->submit();
+  token_scheme_->submit();
   check(ammon_memcpy(rt_.raw(), pinned_logits_, logits_.data(), sizeof(float) * c_.vocab,
                      AMMON_COPY_D2H, stream_),
         "logits");
   check(ammon_stream_synchronize(rt_.raw(), stream_), "step");
-  check_blocks(stream_);
   std::memcpy(host_logits_.data(), pinned_logits_, sizeof(float) * c_.vocab);
   return host_logits_;
 }
@@ -433,7 +220,7 @@ GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prom
   const uint32_t limit = std::min(max_new, c_.max_seq);
   const uint32_t steps = limit > 0 ? limit - 1 : 0;
   const uint32_t n_prompt = (uint32_t)std::min<size_t>(prompt.size(), c_.max_seq);
-  if (!persistent_) ensure_decode_scheme(n_prompt);
+  ensure_decode_scheme(n_prompt);
   ammon_stream st = stream_;
   check(ammon_memcpy(rt_.raw(), prompt_.data(), prompt.data(), sizeof(int32_t) * n_prompt,
                      AMMON_COPY_H2D, st),
@@ -443,15 +230,11 @@ GenerateTokenOutput LlamaModel::generate_device(const std::vector<int32_t> &prom
   check(ammon_event_create(rt_.raw(), &e0), "event");
   check(ammon_event_create(rt_.raw(), &e1), "event");
   for (uint32_t i = 0; i < steps; ++i) {
-    if (persistent_)
-      persistent_->launch(st, true, n_prompt);
-    else
-      decode_scheme_->submit();
+    decode_scheme_->submit();
     if (i == 0) check(ammon_event_record(rt_.raw(), e0, st), "event");
   }
   check(ammon_event_record(rt_.raw(), e1, st), "event");
   check(ammon_stream_synchronize(rt_.raw(), st), "generate");
-  check_blocks(st);
   float ms = 0.f;
   if (steps > 1) check(ammon_event_elapsed_ms(rt_.raw(), e0, e1, &ms), "event");
   ammon_event_destroy(rt_.raw(), e0);
@@ -481,20 +264,14 @@ void LlamaModel::decode(uint32_t token, uint32_t start_pos, uint32_t n_steps, in
   if (token >= c_.vocab) throw Error(AMMON_E_VALIDATION, "decode: token outside the vocab");
   if ((uint64_t)start_pos + n_steps > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "decode: start_pos + n_steps exceeds max_seq");
-  if (!persistent_) ensure_decode_scheme(0);
+  ensure_decode_scheme(0);
   deposit(token, start_pos, stream_);
-  for (uint32_t i = 0; i < n_steps; ++i) {
-    if (persistent_)
-      persistent_->launch(stream_, true, 0);
-    else
-      decode_scheme_->submit();
-  }
+  for (uint32_t i = 0; i < n_steps; ++i) decode_scheme_->submit();
   if (tokens) {
     check(ammon_memcpy(rt_.raw(), tokens, (int32_t *)tokens_.data() + start_pos,
                        sizeof(int32_t) * n_steps, AMMON_COPY_D2H, stream_),
           "tokens");
     check(ammon_stream_synchronize(rt_.raw(), stream_), "decode");
-    check_blocks(stream_);
   }
 }
 
@@ -610,7 +387,7 @@ GenerateTokenOutput LlamaModel::generate_prefill(const std::vector<int32_t> &pro
   const uint32_t n_prompt = (uint32_t)std::min<size_t>(prompt.size(), c_.max_seq);
   // every step is a forced prompt token: nothing to prefill ahead of
   if (steps < n_prompt) return generate_device(prompt, max_new, stop_on, last_logits);
-  if (!persistent_) ensure_decode_scheme(n_prompt);
+  ensure_decode_scheme(n_prompt);
   ammon_runtime *rt = rt_.raw();
   ammon_stream st = stream_;
   prefill(prompt.data(), n_prompt, 0, nullptr);
@@ -631,15 +408,9 @@ GenerateTokenOutput LlamaModel::generate_prefill(const std::vector<int32_t> &pro
   check(ammon_event_create(rt, &e0), "event");
   check(ammon_event_create(rt, &e1), "event");
   check(ammon_event_record(rt, e0, st), "event");
-  for (uint32_t pos = n_prompt; pos < steps; ++pos) {
-    if (persistent_)
-      persistent_->launch(st, true, n_prompt);
-    else
-      decode_scheme_->submit();
-  }
+  for (uint32_t pos = n_prompt; pos < steps; ++pos) decode_scheme_->submit();
   check(ammon_event_record(rt, e1, st), "event");
   check(ammon_stream_synchronize(rt, st), "generate");
-  check_blocks(st);
   float ms = 0.f;
   const uint32_t decoded = steps - n_prompt;
   if (decoded > 0) check(ammon_event_elapsed_ms(rt, e0, e1, &ms), "event");
@@ -668,7 +439,6 @@ void LlamaModel::read_tokens(uint32_t start, uint32_t n, int32_t *out) {
   if ((uint64_t)start + n > c_.max_seq)
     throw Error(AMMON_E_VALIDATION, "tokens: range exceeds max_seq");
   check(ammon_stream_synchronize(rt_.raw(), stream_), "tokens");
-  check_blocks(stream_);
   if (!n) return;
   check(ammon_memcpy(rt_.raw(), out, (int32_t *)tokens_.data() + start, sizeof(int32_t) * n,
                      AMMON_COPY_D2H, stream_),
@@ -876,12 +646,6 @@ ammon_status ammon_llama_launches(ammon_llama *m, uint32_t *n) {
   AMMON_CHECK(m && n, "llama_launches: NULL argument");
   *n = m->model->launches();
   return AMMON_OK;
-}
-
-ammon_status ammon_llama_token_trace(ammon_llama *m, uint64_t *host, size_t capacity,
-                                     uint32_t *slots, uint32_t *workgroups) {
-  AMMON_CHECK(m && slots && workgroups && (host || !capacity), "llama_token_trace: NULL argument");
-  return guarded([&] { m->model->token_trace(host, capacity, slots, workgroups); });
 }
 
 }  // extern "C"

@@ -138,12 +138,7 @@ CausalAttentionBlock::CausalAttentionBlock(const Runtime &rt, uint32_t hidden, u
       opts_.split_len ? opts_.split_len : ammon_attention_default_split(rt.raw(), 1, seq_len);
   max_splits_ = ammon_attention_splits(seq_len, min_split);
   partial_ = Tensor::zeros(rt, Shape::from_dims({query_heads, max_splits_, head_ + 2}), DType::F32);
-  sync_ = Tensor::zeros(rt, Shape::vector(AMMON_BLOCK_SYNC_WORDS), DType::U32);
   table_ = kernels::rope_table(rt, opts.theta, head_, seq_len);
-}
-
-void CausalAttentionBlock::check(ammon_stream stream) const {
-  ammon::check(ammon_block_sync_check(rt_.raw(), stream, (uint32_t *)sync_.data()), "attention");
 }
 
 uint32_t CausalAttentionBlock::split_len_for(uint32_t kv_heads, DType kv_dtype) const {
@@ -197,24 +192,7 @@ void CausalAttentionBlock::record(Scheme &s, TensorView x, const CausalAttention
   float *xb = (float *)xb_.data();
   float *partial = (float *)partial_.data();
   const size_t partial_bytes = partial_.nbytes();
-  uint32_t *sync = (uint32_t *)sync_.data();
   const float *table = (const float *)table_->data();
-  // With one_launch: one launch where its shape contract holds (bf16
-  // weights and cache, head 128, 1-4 q heads per kv head); else the four
-  // launches below.
-  auto block = [=](ammon_stream stream) {
-    return ammon_attention_block(rt, stream, (float *)x.data(), w.norm.data(), abi(w.norm.dtype()),
-                                 eps, w.query.data(), w.key.data(), w.value.data(),
-                                 w.output.data(), abi(w.query.dtype()), hidden, q_heads, kv_heads,
-                                 head, cache.key.data(), cache.value.data(),
-                                 abi(cache.key.dtype()), seq, st, table, split, q, xb, partial,
-                                 partial_bytes, sync);
-  };
-  if (opts_.one_launch && w.output.dtype() == w.query.dtype() &&
-      block(AMMON_STREAM_VALIDATE) == AMMON_OK) {
-    s.record("attention_block", block);
-    return;
-  }
   s.record("qkv_rope_store", [=](ammon_stream stream) {
     return ammon_qkv_rope_store(rt, stream, (const float *)x.data(), w.norm.data(),
                                 abi(w.norm.dtype()), eps, w.query.data(), w.key.data(),
@@ -252,16 +230,10 @@ void CausalAttentionBlock::record_group(Scheme &s, const std::string &label, Ten
 }
 
 // ---- SwiGluBlock ------------------------------------------------------------------------------
-SwiGluBlock::SwiGluBlock(const Runtime &rt, uint32_t hidden, uint32_t intermediate, float eps,
-                         bool one_launch)
-    : rt_(rt), hidden_(hidden), inter_(intermediate), eps_(eps), one_launch_(one_launch) {
+SwiGluBlock::SwiGluBlock(const Runtime &rt, uint32_t hidden, uint32_t intermediate, float eps)
+    : rt_(rt), hidden_(hidden), inter_(intermediate), eps_(eps) {
   need(hidden > 0 && intermediate > 0, "SwiGluBlock: empty shape");
   hb_ = Tensor::zeros(rt, Shape::vector(intermediate), DType::F32);
-  sync_ = Tensor::zeros(rt, Shape::vector(AMMON_BLOCK_SYNC_WORDS), DType::U32);
-}
-
-void SwiGluBlock::check(ammon_stream stream) const {
-  ammon::check(ammon_block_sync_check(rt_.raw(), stream, (uint32_t *)sync_.data()), "ffn");
 }
 
 void SwiGluBlock::record(Scheme &s, TensorView x, const SwiGluBlockWeights &w) const {
@@ -283,18 +255,6 @@ void SwiGluBlock::record(Scheme &s, TensorView x, const SwiGluBlockWeights &w) c
   const uint32_t hidden = hidden_, inter = inter_;
   const float eps = eps_;
   float *hb = (float *)hb_.data();
-  uint32_t *sync = (uint32_t *)sync_.data();
-  // With one_launch: one launch where its shape contract holds (bf16
-  // weights); else the two below.
-  auto block = [=](ammon_stream stream) {
-    return ammon_swiglu_block(rt, stream, (float *)x.data(), w.norm.data(), abi(w.norm.dtype()),
-                              eps, w.gate.data(), w.up.data(), w.down.data(), abi(w.gate.dtype()),
-                              hidden, inter, hb, sync);
-  };
-  if (one_launch_ && w.down.dtype() == w.gate.dtype() && block(AMMON_STREAM_VALIDATE) == AMMON_OK) {
-    s.record("swiglu_block", block);
-    return;
-  }
   s.record("gate_up_swiglu", [=](ammon_stream stream) {
     return ammon_gate_up_swiglu(rt, stream, (const float *)x.data(), w.norm.data(),
                                 abi(w.norm.dtype()), eps, w.gate.data(), w.up.data(),

@@ -162,70 +162,6 @@ typedef struct {
   uint32_t bits; /* fill: raw 32-bit pattern (f32) or 16-bit (bf16) */
 } ammon_k_fill;
 
-/* Fused blocks: one launch per attention block (norm + QKV + RoPE + K/V
- * store, split-K attention, merge, output projection + residual) or SwiGLU
- * block (norm + gate/up + SwiGLU, down projection + residual), the phases
- * separated by grid barriers over `sync` (AMMON_TOKEN_SYNC_WORDS words,
- * zero before a launch and left zero by every launch that completes; the
- * error word is set if a barrier wait gave up). */
-typedef struct {
-  ammon_k_gemv qkv;         /* mode QKV: y = q, caches at step->position */
-  ammon_k_gemv wo;          /* mode RESIDUAL: x += Wo att */
-  ammon_k_attention att;    /* q, caches, partial, out = att */
-  uint32_t *sync;
-  uint32_t spin_limit;
-} ammon_k_attn_block;
-
-typedef struct {
-  ammon_k_gemv gate_up;     /* mode SWIGLU: y = hb */
-  ammon_k_gemv down;        /* mode RESIDUAL: x += W2 hb */
-  uint32_t *sync;
-  uint32_t spin_limit;
-} ammon_k_ffn_block;
-
-/* Persistent decode-token kernel: one cooperative launch runs a whole decode
- * token (embed, every layer, final norm + LM head, optionally the greedy
- * step) with grid-wide barriers between dependent phases.  Per-layer weights
- * are stacked [L, ...]; the caches are [L, kv_heads, seq, head]; sync must
- * not be shared by launches that can run at the same time. */
-#define AMMON_TOKEN_SYNC_ERR (64 * 9) /* word set when a barrier timed out */
-#define AMMON_TOKEN_SYNC_WORDS (64 * 10)
-#define AMMON_TOKEN_GEMV_U 8 /* 16-byte chunks per lane per GEMV tile */
-typedef struct {
-  const void *tok_emb;                 /* [vocab, dim] */
-  const float *rms_att, *rms_ffn;      /* [L, dim] fp32 */
-  const void *wq, *wk, *wv, *wo;       /* [L, q_dim, dim], [L, kv_dim, dim] x2, [L, dim, q_dim] */
-  const void *w1, *w3, *w2;            /* [L, hidden, dim] x2, [L, dim, hidden] */
-  const float *rms_final;              /* [dim] fp32 */
-  const void *wcls;                    /* [vocab, dim] */
-  void *k_cache, *v_cache;             /* [L, kv_heads, seq, head] */
-  const float *table;                  /* RoPE cos/sin [seq, head/2, 2] */
-  ammon_k_step *step;                  /* token/position; advanced by the greedy step */
-  /* Activations, one slice per phase so no address is written after another
-   * workgroup has read it within a launch: x [2L + 1][x_stride] (embed, then
-   * after each attention / FFN residual), q, att [L][q_stride], hb
-   * [L][hb_stride], partial [L][partial_stride]; logits [vocab]. */
-  float *x, *q, *att, *hb, *partial, *logits;
-  uint32_t x_stride, q_stride, hb_stride, partial_stride;
-  float *cand_v;                       /* [gridDim.x] argmax candidates */
-  uint32_t *cand_i;
-  uint32_t *sync;                      /* AMMON_TOKEN_SYNC_WORDS, zero between launches */
-  const int32_t *prompt;               /* greedy: forced tokens, or NULL */
-  int32_t *tokens;                     /* greedy: tokens[pos] = next, or NULL */
-  int32_t *argmax_out;                 /* greedy: the argmax, or NULL */
-  uint32_t dim, n_layers, q_heads, kv_heads, head, hidden, vocab, seq;
-  uint32_t split_len, splits;
-  uint32_t greedy, n_prompt, max_tokens;
-  uint32_t spin_limit;                 /* polls per barrier before giving up */
-  float eps;
-  /* Optional barrier timestamps (s_memrealtime, 100 MHz), or NULL: for
-   * barrier b < trace_slots, trace[2 b G + wg] is when workgroup wg arrived
-   * and trace[(2 b + 1) G + wg] when its wait ended (G = gridDim.x). */
-  uint64_t *trace;
-  uint32_t trace_slots;
-} ammon_k_token;
-
-
 #ifdef __cplusplus
 }
 #endif

@@ -1,5 +1,5 @@
 // argmax_impl.h -- candidate merge of the parallel greedy argmax, shared by
-// misc.hip and token.hip.
+// misc.hip and the LM-head GEMV (gemv_impl.h).
 //
 // sample_argmax (reference src/tokenizer.rs:179-189) returns the first index
 // of the maximum under a strict `>` scan from logits[0]: NaN never wins, and a

@@ -51,31 +51,28 @@ ATT_PARTIAL_G(ammon_attention_partial_bf16_c1, uint16_t, 1)
   ATT_PARTIAL(PREFIX##_g4, KV, CH, 4, 128, true)       \
   ATT_PARTIAL(PREFIX##_g8, KV, CH, 8, 128, true)
 
-// bf16 K/V: q.k on matrix cores with two chunk buffers, one for the 4:1
-// group (the Llama-3 shape): at split 128 every workgroup requesting both of
-// its chunks at once delays all first chunks -- one buffer measured 0.1-0.7
-// us faster per launch at positions 1023..8191 (four buffers no faster than
-// two).  One for the 8:1 group too: 242 VGPRs fit two workgroups per CU,
-// where two buffers (256 VGPRs + 70 AGPRs) fit one, and the Llama-3-70B
-// layer at 32768 positions then steps in 0.623-0.625 ms against 0.635-0.636
-// (each at its best split: 512 against 1024)
-#define ATT_PARTIAL_MFMA(NAME, GMAX, NBUF)                                           \
+ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
+
+// bf16 K/V, head 128: K/V staged in an LDS ring of NCH 64-position chunk
+// buffers by 16-byte buffer-to-LDS requests (AttnPartialMfmaStaged)
+#define ATT_PARTIAL_STAGED(NAME, GMAX, NCH)                                          \
   ATT_KERNEL(NAME) {                                                                \
     ATT_PARAMS(p0);                                                                 \
-    __shared__ float lds[att_lds_floats(GMAX, 8)];                                  \
+    __shared__ float lds[att_staged_lds_floats(GMAX, NCH)];                         \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                    \
-    AttnPartialMfma<GMAX, NBUF> unit;                                               \
-    if (unit.begin(p, blockIdx.x, blockIdx.y))                                      \
+    AttnPartialMfmaStaged<GMAX, NCH> unit;                                          \
+    if (unit.begin(p, blockIdx.x, blockIdx.y, lds))                                 \
       unit.run(p, lds);                                                             \
     else                                                                            \
       direct_out_nan(p, blockIdx.y);                                                \
   }
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g1, 1, 2)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g2, 2, 2)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g4, 4, 1)
-ATT_PARTIAL_MFMA(ammon_attention_partial_h128_bf16_c8_g8, 8, 1)
-ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
-
+#define ATT_PARTIAL_STAGED_G(NCH)                                            \
+  ATT_PARTIAL_STAGED(ammon_attention_partial_h128_bf16_lds##NCH##_g1, 1, NCH) \
+  ATT_PARTIAL_STAGED(ammon_attention_partial_h128_bf16_lds##NCH##_g2, 2, NCH) \
+  ATT_PARTIAL_STAGED(ammon_attention_partial_h128_bf16_lds##NCH##_g4, 4, NCH) \
+  ATT_PARTIAL_STAGED(ammon_attention_partial_h128_bf16_lds##NCH##_g8, 8, NCH)
+ATT_PARTIAL_STAGED_G(1)
+ATT_PARTIAL_STAGED_G(2)
 
 // Merge units of 8 dims: 512 workgroups at the Llama-3-8B shape (32 q
 // heads); measured 3.7 us per launch against 4.2 for 32-dim units.

@@ -1,7 +1,6 @@
 // attention_impl.h -- split-K decode attention with GQA head sharing and a
 // log-sum-exp merge (reference flash-decoding pair, src/kernels.rs:228-410),
-// as workgroup-level units shared by the standalone kernels (attention.hip)
-// and the persistent decode-token kernel (token.hip).
+// as workgroup-level units run by the kernels of attention.hip.
 //
 // Pass 1, one workgroup per (split s, kv head g): positions
 // [s*S, s*S + S) clipped to t <= pos, for all G = q_heads / kv_heads query
@@ -123,8 +122,8 @@ struct AttnPartial {
     for (int r = 0; r < R; ++r) {
       const uint32_t off = off_of(c0 + r * round + wave * PW + slot);
       // the row at the position may have been stored earlier in this launch
-      kr[r] = C::template load_buf<AMMON_HANDOFF_CPOL>(kres, off);
-      vr[r] = C::template load_buf<AMMON_HANDOFF_CPOL>(vres, off);
+      kr[r] = C::template load_buf<0>(kres, off);
+      vr[r] = C::template load_buf<0>(vres, off);
     }
   }
 
@@ -308,62 +307,109 @@ struct AttnPartial {
   }
 };
 
-// Pass 1 on matrix cores, for bf16 K/V and head 128 (Llama-style shapes):
-// the same unit as AttnPartial with q.k on v_mfma_f32_16x16x32_bf16.
+// s_waitcnt that waits until at most N vector-memory operations of this wave
+// are outstanding (expcnt and lgkmcnt left at their maxima; gfx9 encoding:
+// vmcnt bits 3:0 and 15:14).
+template <int N> AMMON_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
+// Compiler-level ordering of LDS accesses between the lanes of one wave: the
+// wave's LDS operations execute in program order, so a value one lane writes
+// is visible to another lane's later read once the compiler keeps the two in
+// that order (no hardware barrier is needed inside a wave).
+AMMON_DEV void wave_lds_order() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// Pass 1 entirely on matrix cores, with K/V staged in LDS by the load unit,
+// for bf16 K/V and head 128 (Llama-style shapes).
 //
-// Chunks of 64 positions, NBUF-buffered in registers (the next NBUF - 1
-// chunks' K and V are in flight while one is processed, so compute on the
-// first chunks of a split overlaps the arrival of the rest; a split of
-// NBUF * 64 positions is requested in one go).  Wave w scores positions
-// [16w, 16w + 16) of a chunk as one 16x16 tile S^T[t][h] = sum_d K[t][d]
-// q[h][d] (A = K rows as stored, B = q^T, heads as the 16 columns; heads
-// >= G are zero).  q is split into bf16 hi + lo parts (two MFMAs per 32
-// dims), so the products keep ~16 mantissa bits of q and accumulate in
-// fp32.  The chunk's scores go to LDS; one wave per head takes the chunk
-// max, rescales the running state and turns scores into weights 2^(s - m)
-// (one exponential per position and head); then every lane accumulates 8
-// dims of V for its 4 positions of the chunk with the weights read from
-// LDS.  All slots share the workgroup's running max, so the final merge
-// across lanes and waves is a plain sum.  The partial format is the VALU
-// unit's: (sum_t e^{s_t - m} V_t, m, l).
-template <int GMAX, int NBUF = 2>
-struct AttnPartialMfma {
+// Staging.  Every K and V request is a 16-byte buffer load written straight
+// into LDS (buffer_load_dwordx4 ... lds), so no VGPRs are held while the
+// bytes are in flight.  The LDS holds a ring of NCH chunk buffers of 64
+// positions (32 KiB each: K and V, 4 waves x 4 requests x 1 KiB); at the
+// start a workgroup requests its first NCH chunks, and each chunk buffer is
+// refilled with the chunk NCH ahead as soon as it is consumed.  Rows past
+// the split's end read zero and touch no memory; the first NCH chunks are
+// always requested, later ones only up to the split's last, so while it
+// processes a chunk a wave has a known number of chunks (8 requests each)
+// in flight behind it, and the waits are compile-time vmcnt values picked
+// by that count.  Each wave
+// reads back only the rows its own requests brought in, so no barrier is
+// needed between the load unit and the consumer beyond the wave's own wait
+// count.
+//
+// Arithmetic.  Wave w owns positions [16w, 16w + 16) of every chunk.
+//   scores  S^T[t][h] = sum_d K[t][d] q[h][d] on v_mfma_f32_16x16x32_bf16
+//           (A = K rows as stored, B = q^T with q split into bf16 hi + lo:
+//           ~16 bits of q, fp32 accumulation); heads >= G are padding;
+//   softmax per wave and head, in base 2: running max m and sum l; the
+//           weights P = 2^(s - m) are exact fp32 values;
+//   values  O^T[d][h] += sum_t V[t][d] P[h][t] on v_mfma_f32_16x16x16_bf16
+//           (A = V^T read from LDS, B = P^T straight from the score tile's
+//           registers -- the score layout of a 16x16 tile is the 16x16x16
+//           B-operand layout), with P split into three bf16 parts
+//           (hi + mid + lo = P exactly), so every product is exact and only
+//           the fp32 summation order differs from the serial definition.
+// So the chunk loop has no workgroup barrier and little VALU work; the four
+// waves' states are merged once at the end: M = max_w m_w,
+// acc = sum_w acc_w 2^(m_w - M), l = sum_w l_w 2^(m_w - M).  The partial
+// format is the other units': (sum_t e^{s_t - m} V_t, m, l).
+//
+// V rows are staged with their 16-byte pieces rotated by 2(row / 4) slots
+// (row = the wave's position 0..15), so the 16-bit column reads of the four
+// lane groups (rows 4g + i) fall in distinct LDS banks.
+//
+// LDS: att_staged_lds_floats(GMAX, NCH) floats (the merge's rows reuse the
+// chunk buffers).
+#define ATT_STAGED_OROW (ATT_MAX_HEAD + 1)  // padded merge row (bank spread)
+
+// Max / sum over lanes l and l ^ 32 (resp. l ^ 16) with gfx950's lane-swap
+// instructions (VALU, no LDS round trip): permlane32_swap(v, v) leaves the
+// lane's own value in one result and its partner's in the other, so both
+// lanes of a pair compute the same max and the same (commutative) sum.
+AMMON_DEV float pair32_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+AMMON_DEV float pair16_max(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+AMMON_DEV float pair32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+AMMON_DEV float pair16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+constexpr uint32_t att_staged_lds_floats(int GMAX, int NCH) {
+  const uint32_t ring = (uint32_t)NCH * 8192u;                      // NCH x 32 KiB
+  const uint32_t merge = AMMON_WAVES * GMAX * ATT_STAGED_OROW;      // per-wave outputs
+  return (ring > merge ? ring : merge) + 2 * AMMON_WAVES * GMAX;
+}
+
+template <int GMAX, int NCH>
+struct AttnPartialMfmaStaged {
   static_assert(GMAX >= 1 && GMAX <= 16, "q heads per kv head");
-  static_assert(NBUF >= 1 && NBUF <= 4, "chunk buffers");
+  static_assert(NCH >= 1 && NCH <= 4, "chunk buffers");
   static constexpr uint32_t HEAD = 128, CHUNK = 64;
+  static constexpr int REQ = 8;  // requests per wave per chunk (4 K + 4 V)
   typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+  typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
   typedef float f32x8 __attribute__((ext_vector_type(8)));
 
   uint32_t split, g, pos, t0, n, lane, wave;
   __amdgpu_buffer_rsrc_t kres, vres;
-  // q^T (B operand): lane l holds head l % 16, dims 32(l/16) + 8kk..+7 as fp32
   float4 qraw[4][2];
-  // per chunk buffer: K row (l % 16) of the wave's tile, dims 32(l/16) + 8kk;
-  // V rows of the lane's 4 positions 16w + 4k + l/16, dims 8(l % 16)..+7
-  u32x4 kb[NBUF][4], vb[NBUF][4];
 
-  // Positions past the split read zero without touching memory, so loads
-  // are issued unconditionally and the wait counts stay exact.
-  // Rows at or past `rows` (of the split) read as zero.
-  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4], uint32_t rows) const {
-    const uint32_t tk = c0 + 16 * wave + (lane & 15);
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      const uint32_t off = tk < rows ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
-      kr[kk] = __builtin_amdgcn_raw_buffer_load_b128(kres, off, 0, AMMON_HANDOFF_CPOL);
-    }
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t tv = c0 + 16 * wave + 4 * k + (lane >> 4);
-      const uint32_t off = tv < rows ? (tv * HEAD + 8 * (lane & 15)) * 2 : AMMON_OOB;
-      vr[k] = __builtin_amdgcn_raw_buffer_load_b128(vres, off, 0, AMMON_HANDOFF_CPOL);
-    }
-  }
-  AMMON_DEV void load_chunk(uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) const {
-    load_chunk(c0, kr, vr, n);
-  }
-
-  // The unit's split and cache resources; false for a dead split (start past
+  // The split, its cache resources and q; false for a dead split (start past
   // the position) or an out-of-range position, which write nothing.
   AMMON_DEV bool setup(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
     split = split_;
@@ -380,9 +426,41 @@ struct AttnPartialMfma {
     return true;
   }
 
+  // Ring buffer b's K (kv 0) or V (kv 1) block of request i of wave w, as
+  // 16-byte slots: lane l's bytes land at slot l.
+  AMMON_DEV static u32x4 *slot_base(float *lds, uint32_t b, uint32_t kv, uint32_t w, uint32_t i) {
+    return (u32x4 *)lds + ((b * 2 + kv) * 16 + w * 4 + i) * 64;
+  }
+
+  // Request chunk c of the split into ring buffer b.  K: request kk brings
+  // row 16w + (l % 16) of the chunk, dims 32(l / 16) + 8kk..+7 (the score
+  // MFMA's A fragment of lane l).  V: request i brings row r = 4i + l / 16
+  // of the wave's 16, 16-byte piece (l % 16 + 2i) % 16 -- so the wave's V
+  // block is [row][slot], slot s of row r holding dims 8((s + 2(r / 4)) %
+  // 16)..+7.  Rows at or past the split's end read as zero.
+  AMMON_DEV void stage(float *lds, uint32_t c, uint32_t b) const {
+    const uint32_t c0 = c * CHUNK + 16 * wave;
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      const uint32_t tk = c0 + (lane & 15);
+      const uint32_t off = tk < n ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          kres, (__attribute__((address_space(3))) void *)slot_base(lds, b, 0, wave, kk), 16,
+          off, 0, 0, 0);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t tv = c0 + 4 * i + (lane >> 4);
+      const uint32_t piece = ((lane & 15) + 2 * i) & 15;
+      const uint32_t off = tv < n ? (tv * HEAD + 8 * piece) * 2 : AMMON_OOB;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          vres, (__attribute__((address_space(3))) void *)slot_base(lds, b, 1, wave, i), 16,
+          off, 0, 0, 0);
+    }
+  }
+
   // Lanes of score columns h >= GMAX load head 0's q: those columns are
-  // never stored, and unconditional loads leave no branch whose join would
-  // wait for the first loads before the K/V requests go out.
+  // never used, and unconditional loads keep the wait counts exact.
   AMMON_DEV void load_q(const ammon_k_attention &p) {
     const uint32_t h = lane & 15;
     const float *qp = p.q + (size_t)(g * GMAX + (h < GMAX ? h : 0)) * HEAD + 32 * (lane >> 4);
@@ -393,49 +471,48 @@ struct AttnPartialMfma {
     }
   }
 
-  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
+  // q first (loads complete in order: the q conversion then waits for q
+  // alone), then chunks 0..NCH - 1 -- unconditionally, so the count of
+  // requests behind q is fixed (chunks past a short split read zero and
+  // touch no memory).
+  AMMON_DEV bool begin(const ammon_k_attention &p, uint32_t split_, uint32_t g_, float *lds) {
     if (!setup(p, split_, g_)) return false;
-    // q first: loads complete in order, so the first chunk's MFMAs then wait
-    // only for q and that chunk, not for the later chunk's K/V as well
     load_q(p);
 #pragma unroll
-    for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b]);
-    // keep run()'s q conversion below the requests: scheduled among them,
-    // it waited for q before the later K/V requests went out
+    for (int b = 0; b < NCH; ++b) stage(lds, b, b);
     __builtin_amdgcn_sched_barrier(0);
     return true;
   }
 
-  // begin() in two steps, for a caller whose q and newest K/V row are stored
-  // by other workgroups of the same launch: prefetch() -- before they are --
-  // requests the first NBUF chunks with every row except the position's
-  // (which may not exist yet); finish() -- once they are -- requests q and,
-  // if the position's row lies in a prefetched chunk, that chunk again in
-  // full.  run() then sees exactly what begin() would have loaded.
-  AMMON_DEV bool prefetch(const ammon_k_attention &p, uint32_t split_, uint32_t g_) {
-    if (!setup(p, split_, g_)) return false;
-    const uint32_t before = t0 + n - 1 == pos ? n - 1 : n;  // rows older than the position
-#pragma unroll
-    for (int b = 0; b < NBUF; ++b) load_chunk(b * CHUNK, kb[b], vb[b], before);
-    return true;
-  }
-  AMMON_DEV void finish(const ammon_k_attention &p) {
-    load_q(p);
-    if (t0 + n - 1 == pos) {
-      const uint32_t cb = (pos - t0) / CHUNK;  // chunk of the position's row
-#pragma unroll
-      for (int b = 0; b < NBUF; ++b)
-        if ((uint32_t)b == cb) load_chunk(b * CHUNK, kb[b], vb[b]);
-    }
+  // Wait until at most `extra` requests plus k whole chunks (REQ each) of
+  // this wave are outstanding, k = 0..NCH - 1 (the chunks requested after
+  // the one being processed).
+  template <int EXTRA> AMMON_DEV static void wait_chunks(uint32_t k) {
+    if (NCH > 3 && k == 3) wait_vmcnt<EXTRA + 3 * REQ>();
+    else if (NCH > 2 && k == 2) wait_vmcnt<EXTRA + 2 * REQ>();
+    else if (NCH > 1 && k == 1) wait_vmcnt<EXTRA + REQ>();
+    else wait_vmcnt<EXTRA>();
   }
 
-  // lds: att_lds_floats(GMAX, 8) floats.
+  // The V^T A fragment of dims 16nt..16nt+15 from the wave's staged V block:
+  // lane l gets V[4(l / 16) + i][16nt + l % 16], i = 0..3.
+  AMMON_DEV static i16x4 v_frag(const float *vblk, uint32_t lane, int nt) {
+    const uint16_t *v = (const uint16_t *)vblk;
+    const uint32_t grp = lane >> 4, d = 16 * nt + (lane & 15);
+    // row 4 grp + i sits at rotation 2 grp: slot (d / 8 - 2 grp) % 16
+    const uint32_t col = ((((d >> 3) - 2 * grp) & 15) << 3) | (d & 7);
+    i16x4 f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = (short)v[(4 * grp + i) * HEAD + col];
+    return f;
+  }
+
   AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
-    float(*s_red)[GMAX * 8 + 1] = (float(*)[GMAX * 8 + 1])lds;      // final merge
-    float *s_s = lds + AMMON_WG * (GMAX * 8 + 1);                     // [CHUNK][GMAX]
-    float *s_scale = s_s + CHUNK * GMAX;                              // [GMAX]
-    float *s_ml = s_scale + GMAX;                                     // [2][GMAX]
+    const uint32_t ring = att_staged_lds_floats(GMAX, NCH) - 2 * AMMON_WAVES * GMAX;
+    float *s_m = lds + ring;                                       // [4][GMAX] wave maxima
+    float *s_l = s_m + AMMON_WAVES * GMAX;                         // [4][GMAX] wave sums
     const float scale2 = 1.4426950408889634f / sqrtf((float)HEAD);  // log2(e)/sqrt(head)
+    const uint32_t h = lane & 15, grp = lane >> 4;
 
     // q^T as bf16 hi + lo B operands
     bf16x8 qhi[4], qlo[4];
@@ -443,140 +520,164 @@ struct AttnPartialMfma {
     for (int kk = 0; kk < 4; ++kk) {
       const float4 a = qraw[kk][0], b = qraw[kk][1];
       const f32x8 f = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-      // v_cvt_pk_bf16_f32 (round to nearest even); hi + lo = q to ~16 bits
       qhi[kk] = __builtin_convertvector(f, bf16x8);
       qlo[kk] = __builtin_convertvector(f - __builtin_convertvector(qhi[kk], f32x8), bf16x8);
     }
 
-    float acc[GMAX][8];
+    // O^T tiles: lane l holds dims 16nt + 4(l / 16) + r of head l % 16
+    f32x4 o[8];
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[j][e] = 0.f;
-    // running max / sum of the heads this wave owns: h = wave + 4i
-    constexpr int HW = (GMAX + AMMON_WAVES - 1) / AMMON_WAVES;
-    float m_run[HW], l_run[HW];
-#pragma unroll
-    for (int i = 0; i < HW; ++i) {
-      m_run[i] = -INFINITY;
-      l_run[i] = 0.f;
-    }
+    for (int nt = 0; nt < 8; ++nt) o[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // running max / sum of head h (the lanes of one head agree)
+    float m_run = -INFINITY, l_run = 0.f;
 
-    auto process = [&](uint32_t c0, u32x4 (&kr)[4], u32x4 (&vr)[4]) {
-      // scores of this wave's 16-position tile
-      f32x4 st = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int kk = 0; kk < 4; ++kk) {
-        const bf16x8 a = __builtin_bit_cast(bf16x8, kr[kk]);
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], st, 0, 0, 0);
-        st = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], st, 0, 0, 0);
-      }
-      if (c0 > 0) __syncthreads();  // previous chunk's weights consumed
-      // D layout: lane l holds S^T[4(l/16) + r][l % 16] of the tile
-      if ((lane & 15) < GMAX) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t pl = 16 * wave + 4 * (lane >> 4) + r;  // position in chunk
-          // score (reference src/kernels.rs:298: dot / sqrt(head)), base-2 units
-          s_s[pl * GMAX + (lane & 15)] = c0 + pl < n ? st[r] * scale2 : -INFINITY;
-        }
-      }
-      __syncthreads();
-      // one wave per head: chunk max, running rescale, weights
-#pragma unroll
-      for (int i = 0; i < HW; ++i) {
-        const uint32_t h = wave + AMMON_WAVES * i;
-        if (h >= GMAX) continue;  // wave-uniform
-        const float a0 = s_s[lane * GMAX + h];
-        const float mc = wave_max(a0);
-        const float m_new = fmaxf(m_run[i], mc);
-        // m_new is finite: every chunk holds at least one valid position
-        const float sc = __builtin_amdgcn_exp2f(m_run[i] - m_new);  // 0 on the first chunk
-        const float e0 = __builtin_amdgcn_exp2f(a0 - m_new);
-        s_s[lane * GMAX + h] = e0;
-        const float ls = wave_sum(e0);
-        l_run[i] = l_run[i] * sc + ls;
-        m_run[i] = m_new;
-        if (lane == 0) s_scale[h] = sc;
-      }
-      __syncthreads();
-      // V: lane l accumulates dims 8(l % 16)..+7 of positions 16w + 4k + l/16
-#pragma unroll
-      for (int j = 0; j < GMAX; ++j) {
-        const float sc = s_scale[j];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) acc[j][e] *= sc;
-      }
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t pl = 16 * wave + 4 * k + (lane >> 4);
-        float vf[8];
-        Chunk<uint16_t, 8>::widen(vr[k], vf);
-#pragma unroll
-        for (int j = 0; j < GMAX; ++j) {
-          const float w = s_s[pl * GMAX + j];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[j][e] += w * vf[e];
-        }
-      }
-    };
-
-    // Buffers keep fixed roles (unrolled); each is refilled NBUF chunks
-    // ahead.  Steady state while every refill lies inside the split; the
-    // last 2 NBUF - 1 chunks at most run in two passes, the second without
-    // prefetches: a load past the split returns only zeros, but the merge
-    // below reuses its registers and would first wait for it to come back.
     const uint32_t nch = (n + CHUNK - 1) / CHUNK;
-    uint32_t c = 0;  // chunk index
-    for (; c + 2 * NBUF <= nch; c += NBUF) {
+    // The split in blocks of up to NCH chunks (the whole split when it fits
+    // the ring): all scores of a block first, then one max / exponential
+    // pass, then the block's values -- the running state is rescaled once
+    // per block, not per chunk.  Chunk c + NCH is requested once chunk c's
+    // values are done, so when a block starts its chunks are requested and
+    // the next block's are not: chunks [0, base_end) are, base_end = NCH for
+    // the first block (chunks past a short split included) and the block's
+    // end for the others.
+    for (uint32_t c0b = 0; c0b < nch; c0b += NCH) {
+      const uint32_t base_end = c0b == 0 ? (uint32_t)NCH : min(c0b + NCH, nch);
+      float sb[NCH][4];
 #pragma unroll
-      for (int b = 0; b < NBUF; ++b) {
-        process((c + b) * CHUNK, kb[b], vb[b]);
-        load_chunk((c + b + NBUF) * CHUNK, kb[b], vb[b]);
+      for (int i = 0; i < NCH; ++i) {
+        const uint32_t c = c0b + i;
+        if (c >= nch) {  // past the split (uniform)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) sb[i][r] = -INFINITY;
+          continue;
+        }
+        // K of chunk c landed: only its V and the block's later chunks may
+        // be outstanding
+        wait_chunks<4>(base_end - 1 - c);
+        // two independent accumulation chains (q hi and q lo parts)
+        f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+          const bf16x8 a = __builtin_bit_cast(bf16x8, slot_base(lds, c % NCH, 0, wave, kk)[lane]);
+          sh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], sh, 0, 0, 0);
+          sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], sl, 0, 0, 0);
+        }
+        const f32x4 st = sh + sl;
+        // lane l holds S^T[4(l / 16) + r][l % 16]: head h, positions
+        // 16w + 4 grp + r of the chunk.  Score (reference
+        // src/kernels.rs:298: dot / sqrt(head)) in base-2 units; past the
+        // split: -inf.
+        const uint32_t pl0 = c * CHUNK + 16 * wave + 4 * grp;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sb[i][r] = pl0 + r < n ? st[r] * scale2 : -INFINITY;
+      }
+      float mc = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i)
+        mc = fmaxf(mc, fmaxf(fmaxf(sb[i][0], sb[i][1]), fmaxf(sb[i][2], sb[i][3])));
+      mc = pair32_max(pair16_max(mc));
+      const float m_new = fmaxf(m_run, mc);
+      // a wave with no position yet keeps (m, l, acc) = (-inf, 0, 0)
+      const float m_use = m_new == -INFINITY ? 0.f : m_new;
+      const float sc = __builtin_amdgcn_exp2f(m_run - m_use);
+      f32x4 pr[NCH];
+      float ls = 0.f;
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) pr[i][r] = __builtin_amdgcn_exp2f(sb[i][r] - m_use);
+        ls += (pr[i][0] + pr[i][1]) + (pr[i][2] + pr[i][3]);
+      }
+      ls = pair32_sum(pair16_sum(ls));
+      l_run = l_run * sc + ls;
+      m_run = m_new;
+      // rescale the running tiles (none before the first block; a multiply
+      // by exactly 1 is skipped)
+      if (c0b > 0 && !__all(sc == 1.0f)) {
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) o[nt] *= sc;
+      }
+#pragma unroll
+      for (int i = 0; i < NCH; ++i) {
+        const uint32_t c = c0b + i;
+        if (c >= nch) continue;  // uniform
+        // P^T as three bf16 parts with hi + mid + lo = P exactly
+        i16x4 pp[3];
+        const bf16x4 phi = __builtin_convertvector(pr[i], bf16x4);
+        const f32x4 r1 = pr[i] - __builtin_convertvector(phi, f32x4);
+        const bf16x4 pmid = __builtin_convertvector(r1, bf16x4);
+        pp[0] = __builtin_bit_cast(i16x4, phi);
+        pp[1] = __builtin_bit_cast(i16x4, pmid);
+        pp[2] = __builtin_bit_cast(
+            i16x4, __builtin_convertvector(r1 - __builtin_convertvector(pmid, f32x4), bf16x4));
+        // V of chunk c landed: the block's later chunks and the refills for
+        // its earlier ones (chunks up to min(c + NCH, nch)) may be
+        // outstanding
+        wait_chunks<0>(max(base_end, min(c + NCH, nch)) - 1 - c);
+        const float *vblk = (const float *)slot_base(lds, c % NCH, 1, wave, 0);
+        i16x4 va[8];
+#pragma unroll
+        for (int nt = 0; nt < 8; ++nt) va[nt] = v_frag(vblk, lane, nt);
+        // part-major: eight independent accumulation chains per part
+#pragma unroll
+        for (int part = 0; part < 3; ++part)
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt)
+            o[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va[nt], pp[part], o[nt], 0, 0, 0);
+        // refill buffer c % NCH with chunk c + NCH once this wave's reads
+        // of it have returned (lgkmcnt(0); vmcnt and expcnt at their maxima)
+        if (c + NCH < nch) {
+          wave_lds_order();
+          __builtin_amdgcn_s_waitcnt(0xC07F);
+          stage(lds, c + NCH, c % NCH);
+        }
       }
     }
-#pragma unroll
-    for (int b = 0; b < NBUF; ++b) {
-      if (c + b < nch) {
-        process((c + b) * CHUNK, kb[b], vb[b]);
-        if (c + b + NBUF < nch) load_chunk((c + b + NBUF) * CHUNK, kb[b], vb[b]);
-      }
-    }
-#pragma unroll
-    for (int b = 0; b < NBUF; ++b)
-      if (c + NBUF + b < nch) process((c + NBUF + b) * CHUNK, kb[b], vb[b]);
 
-    // merge: plain sums over the 16 position slots (4 per wave) of the group
+    // every request has landed (zero-filled chunks of a short split too)
+    // before the ring's LDS is reused below
+    wait_vmcnt<0>();
+    if (lane < GMAX) {
+      s_m[wave * GMAX + lane] = m_run;
+      s_l[wave * GMAX + lane] = l_run;
+    }
     __syncthreads();
+    // this wave's tiles, scaled to the workgroup max, as rows [w][h][d]
+    if (h < GMAX) {
+      float M = s_m[h];
 #pragma unroll
-    for (int j = 0; j < GMAX; ++j)
+      for (int w = 1; w < AMMON_WAVES; ++w) M = fmaxf(M, s_m[w * GMAX + h]);
+      // M is finite: a live split's first position is wave 0's
+      const float f = __builtin_amdgcn_exp2f(m_run - M);
+      float *row = lds + (wave * GMAX + h) * ATT_STAGED_OROW + 4 * grp;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) s_red[threadIdx.x][j * 8 + e] = acc[j][e];
+      for (int nt = 0; nt < 8; ++nt)
 #pragma unroll
-    for (int i = 0; i < HW; ++i) {
-      const uint32_t h = wave + AMMON_WAVES * i;
-      if (h < GMAX && lane == 0) {
-        s_ml[h] = m_run[i];
-        s_ml[GMAX + h] = l_run[i];
-      }
+        for (int r = 0; r < 4; ++r) row[16 * nt + r] = o[nt][r] * f;
     }
     __syncthreads();
     const uint32_t slot_w = HEAD + 2;
     for (uint32_t idx = threadIdx.x; idx < GMAX * HEAD; idx += AMMON_WG) {
       const uint32_t j = idx / HEAD, d = idx % HEAD;
-      const uint32_t sb = d / 8, e = d % 8;
       float total = 0.f;
 #pragma unroll
-      for (uint32_t s = 0; s < 16; ++s) total += s_red[(s >> 2) * 64 + (s & 3) * 16 + sb][j * 8 + e];
+      for (int w = 0; w < AMMON_WAVES; ++w) total += lds[(w * GMAX + j) * ATT_STAGED_OROW + d];
+      float M = s_m[j];
+#pragma unroll
+      for (int w = 1; w < AMMON_WAVES; ++w) M = fmaxf(M, s_m[w * GMAX + j]);
+      float L = 0.f;
+#pragma unroll
+      for (int w = 0; w < AMMON_WAVES; ++w)
+        L += s_l[w * GMAX + j] * __builtin_amdgcn_exp2f(s_m[w * GMAX + j] - M);
       if (direct_out(p)) {  // the only split: the merge's result, total / l
-        st_out(p.out + (size_t)(g * GMAX + j) * HEAD + d, total / s_ml[GMAX + j]);
+        st_out(p.out + (size_t)(g * GMAX + j) * HEAD + d, total / L);
         continue;
       }
-      float *o = p.partial + ((size_t)(g * GMAX + j) * p.splits + split) * slot_w;
-      st_out(o + d, total);
+      float *o_ = p.partial + ((size_t)(g * GMAX + j) * p.splits + split) * slot_w;
+      st_out(o_ + d, total);
       if (d == 0) {
-        st_out(o + HEAD, s_ml[j] * 0.6931471805599453f);  // back to natural-log units
-        st_out(o + HEAD + 1, s_ml[GMAX + j]);
+        st_out(o_ + HEAD, M * 0.6931471805599453f);  // back to natural-log units
+        st_out(o_ + HEAD + 1, L);
       }
     }
   }

@@ -31,54 +31,23 @@ AMMON_DEV void store_elem(void *base, uint32_t dtype, size_t i, float v) {
     ((float *)base)[i] = v;
 }
 
-// Hand-off of results between workgroups.  Standalone kernels hand results
-// over at kernel boundaries only: plain stores (complete at L2) and plain
-// loads.  A code object whose workgroups hand results to each other inside
-// one launch (the persistent token kernel) defines AMMON_AGENT_HANDOFF to 1
-// before including this header; then
-//   - outputs (activations, K/V rows, partials, candidates) are stored at
-//     agent scope (global_store ... sc1): written through to the device
-//     coherence point, never left dirty in one XCD's L2;
-//   - every load of a value another workgroup wrote in the same launch is an
-//     agent-scope load (sc1: ld_in / ld_in4 / AMMON_HANDOFF_CPOL on buffer
-//     loads), which the memory model makes coherent per location -- it cannot
-//     return a stale line from this CU's L1 or this XCD's L2, whatever lines
-//     (shared with other slices, or cached by earlier reads) they hold.
-// A grid barrier between producer and consumer orders the two: producers
-// wait for their stores to complete (s_waitcnt) before counting in, and
-// consumers issue these loads only after the count is seen.
-#ifndef AMMON_AGENT_HANDOFF
-#define AMMON_AGENT_HANDOFF 0
-#endif
-#define AMMON_HANDOFF_CPOL (AMMON_AGENT_HANDOFF ? 16 : 0)  // buffer-load aux: sc1
+// Results pass between kernels at kernel boundaries only: outputs are plain
+// stores (st_out) and inputs another kernel wrote are plain loads (ld_in,
+// ld_in4).
 // Weight matrices are streamed once per token: nontemporal buffer loads
 // (aux 2 = nt).  Measured at the Llama-3-8B shape: gate/up 40.7 -> 38.0 us,
 // LM head 178 -> 163 us.
 #define AMMON_WEIGHT_CPOL 2
 template <typename T>
 AMMON_DEV void st_out_t(T *p, T v) {
-  if (AMMON_AGENT_HANDOFF)
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  else
-    *p = v;
+  *p = v;
 }
-// Load of a value another workgroup may have written in this launch.
 template <typename T>
 AMMON_DEV T ld_in(const T *p) {
-  if (AMMON_AGENT_HANDOFF) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return *p;
 }
-// ... four floats at a 16-byte-aligned address (two 8-byte agent loads).
-AMMON_DEV float4 ld_in4(const float *p) {
-  if (AMMON_AGENT_HANDOFF) {
-    const uint64_t a = __hip_atomic_load((const uint64_t *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const uint64_t b =
-        __hip_atomic_load((const uint64_t *)p + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    return make_float4(__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32)),
-                       __uint_as_float((uint32_t)b), __uint_as_float((uint32_t)(b >> 32)));
-  }
-  return *(const float4 *)p;
-}
+// ... four floats at a 16-byte-aligned address
+AMMON_DEV float4 ld_in4(const float *p) { return *(const float4 *)p; }
 AMMON_DEV void st_out(float *p, float v) { st_out_t(p, v); }
 AMMON_DEV void st_out(uint32_t *p, uint32_t v) { st_out_t(p, v); }
 AMMON_DEV void st_out(int32_t *p, int32_t v) { st_out_t(p, v); }
@@ -183,7 +152,7 @@ template <> struct Chunk<float, 4> {
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
-  static AMMON_DEV V load_in(const float *p) {  // handed-off data (ld_in4)
+  static AMMON_DEV V load_in(const float *p) {  // another kernel's output (ld_in4)
     const float4 v = ld_in4(p);
     return V{v.x, v.y, v.z, v.w};
   }
@@ -199,7 +168,7 @@ template <> struct Chunk<float, 2> {
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *(const V *)p; }
-  static AMMON_DEV V load_in(const float *p) {  // handed-off data (8-byte agent load)
+  static AMMON_DEV V load_in(const float *p) {  // another kernel's output (8-byte load)
     const uint64_t a = ld_in((const uint64_t *)p);
     return V{__uint_as_float((uint32_t)a), __uint_as_float((uint32_t)(a >> 32))};
   }
@@ -215,7 +184,7 @@ template <> struct Chunk<float, 1> {
     return __builtin_bit_cast(V, __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, CPOL));
   }
   static AMMON_DEV V load(const float *p) { return *p; }
-  static AMMON_DEV V load_in(const float *p) { return ld_in(p); }  // handed-off data
+  static AMMON_DEV V load_in(const float *p) { return ld_in(p); }  // another kernel's output
   static AMMON_DEV V load_nt(const float *p) { return *p; }
   static AMMON_DEV V zero() { return 0.f; }
   static AMMON_DEV void widen(V v, float *f) { f[0] = v; }

@@ -1,6 +1,5 @@
-// gemv_impl.h -- the bandwidth-bound batch-1 GEMV pass shared by the
-// standalone GEMV kernels (gemv.hip) and the persistent decode-token kernel
-// (token.hip).  Replaces the reference's Goldy matmul_into
+// gemv_impl.h -- the bandwidth-bound batch-1 GEMV pass of the GEMV kernels
+// (gemv.hip).  Replaces the reference's Goldy matmul_into
 // (src/kernels.rs:518-528), whose definition is the serial gemv
 // (src/kernels.rs:54-73), with the surrounding rmsnorm / rope_store /
 // cache_store / swiglu / add_into launches of src/blocks.rs:219-276 fused in.
@@ -31,17 +30,15 @@
 //             rotated k and raw v go to the head-major caches at that position
 //             (src/kernels.rs:174-226).
 //
-// The pass is split in two so a caller can start streaming weights before
-// x exists: begin() requests the first two tiles (weights only), run()
-// stages x, then multiplies and keeps streaming.  Work is a sequence of
+// The pass runs in two steps: begin() requests the first two tiles (weights
+// only, which depend on nothing an earlier kernel wrote), run() stages x,
+// then multiplies and keeps streaming.  Work is a sequence of
 // tiles per workgroup: tile = (row block, chunk range) of RPW rows per wave
 // x 64*U chunks, software-pipelined through two register buffers -- the
 // next tile's loads are in flight while the current one is multiplied.
 //
-// Outputs (y, K/V rows) go through st_out and inputs another workgroup may
-// have written (x, the residual) through ld_in: plain accesses in the
-// standalone kernels, agent-scope ones where workgroups hand results to
-// each other inside a launch (device_common.h, AMMON_AGENT_HANDOFF).
+// Outputs (y, K/V rows) go through st_out and inputs an earlier kernel
+// wrote (x, the residual) through ld_in (device_common.h).
 //
 // The RMSNorm prologue sums squares with the same per-lane chunking and
 // reduction order as ammon_rmsnorm, so its normalised x matches the
@@ -208,7 +205,7 @@ struct GemvPass {
           const uint32_t q = g * GQ + (GQ == 128 ? 2 * lane + pl : lane);
           __builtin_amdgcn_raw_ptr_buffer_load_lds(
               xres, (__attribute__((address_space(3))) void *)(xs4 + g * GQ + pl * 64), 16,
-              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, AMMON_HANDOFF_CPOL);
+              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, 0);
         }
       }
       __builtin_amdgcn_s_waitcnt(0);

@@ -29,7 +29,10 @@ struct Kernels {
   hipFunction_t cache_store = nullptr;
   hipFunction_t att_partial[2][kAttChunks][kAttGroups] = {};
   // head-128 specialisations: [dtype][group index], widest chunk only
-  hipFunction_t att_partial_h128[2][kAttGroups] = {};
+  // head 128, power-of-two group: fp32 caches on VALU; bf16 caches on
+  // matrix cores with K/V staged in an LDS ring of 1 or 2 chunk buffers
+  hipFunction_t att_partial_h128_f32[kAttGroups] = {};
+  hipFunction_t att_partial_staged[2][kAttGroups] = {};
   hipFunction_t att_combine = nullptr;
   hipFunction_t att_combine_waves = nullptr;  // one wave per (token, q head)
   hipFunction_t gemv[2][2][kGemvModes] = {};
@@ -42,11 +45,6 @@ struct Kernels {
   hipFunction_t fill_normal = nullptr;
   hipFunction_t fill_const = nullptr;
   hipFunction_t checksum = nullptr;
-  // one-launch blocks (bf16): attention [G index 1, 2, 4], SwiGLU
-  hipFunction_t attn_block[kAttGroups] = {};
-  hipFunction_t ffn_block = nullptr;
-  // persistent decode-token kernel (bf16 weights, head 128): [kv dtype][G index]
-  hipFunction_t token[2][kAttGroups] = {};
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]
   // [row tile per wave / split over the workgroup's waves][mode]
   hipFunction_t gemm[2][2][2][kGemvModes] = {};

@@ -15,10 +15,6 @@
 
 using namespace ammon_rt;
 
-static_assert(AMMON_BLOCK_SYNC_WORDS == AMMON_TOKEN_SYNC_WORDS &&
-                  AMMON_BLOCK_SYNC_ERR == AMMON_TOKEN_SYNC_ERR,
-              "block barrier words: one layout for the header and the kernels");
-
 namespace {
 
 using DeviceGuard = ammon_rt::DeviceScope;
@@ -240,8 +236,11 @@ int att_group_index(uint32_t g) {
 }
 
 // Pass-1 variant for a cache layout, or NULL when no chunk width fits.
+// split_len 0: the kernel a split of 128 positions would take (occupancy
+// queries before the split is chosen).
 hipFunction_t attention_kernel(ammon_runtime *rt, ammon_dtype kv_dtype, uint32_t q_heads,
-                               uint32_t kv_heads, uint32_t head, const void *k, const void *v) {
+                               uint32_t kv_heads, uint32_t head, const void *k, const void *v,
+                               uint32_t split_len) {
   const int ci = att_chunk_index(kv_dtype, head, k, v);
   if (ci < 0) return nullptr;
   const int gi = att_group_index(q_heads / kv_heads);
@@ -249,7 +248,14 @@ hipFunction_t attention_kernel(ammon_runtime *rt, ammon_dtype kv_dtype, uint32_t
   const uint32_t g = q_heads / kv_heads;
   // head 128, widest chunk, power-of-two group: the compile-time variant
   const bool h128 = head == 128 && ci == (dt ? 0 : 1) && (g & (g - 1)) == 0;
-  return h128 ? rt->k.att_partial_h128[dt][gi] : rt->k.att_partial[dt][ci][gi];
+  if (h128 && dt) {
+    // LDS chunk buffers: one for a split of one 64-position chunk, else two
+    // (a split of up to two chunks is requested whole at the start; longer
+    // ones stream through the ring)
+    const uint32_t chunks = split_len ? (split_len + 63) / 64 : 2;
+    return rt->k.att_partial_staged[chunks >= 2 ? 1 : 0][gi];
+  }
+  return h128 ? rt->k.att_partial_h128_f32[gi] : rt->k.att_partial[dt][ci][gi];
 }
 
 ammon_status attention_check(ammon_runtime *rt, const char *what, uint32_t q_heads,
@@ -391,7 +397,8 @@ ammon_status attention_pass1(ammon_runtime *rt, ammon_stream stream, const float
   AMMON_CHECK(valid_dtype(kv_dtype), "attention_partial: unknown kv dtype %d", (int)kv_dtype);
   ammon_status st = attention_check(rt, "attention_partial", q_heads, kv_heads, head, seq, split_len);
   if (st != AMMON_OK) return st;
-  hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache);
+  hipFunction_t f =
+      attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache, split_len);
   AMMON_CHECK(f, "attention_partial: head %u needs an even width above 64", head);
   VALIDATE_ONLY();
   const uint32_t splits = ammon_attention_splits(seq, split_len);
@@ -457,7 +464,8 @@ uint32_t ammon_attention_default_split_for(ammon_runtime *rt, uint32_t q_heads,
   if (rt && kv_heads > 0 && q_heads % kv_heads == 0 && q_heads / kv_heads <= 8 && head > 0 &&
       head <= AMMON_ATTENTION_MAX_HEAD && valid_dtype(kv_dtype)) {
     DeviceGuard guard(rt->device);
-    hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, nullptr, nullptr);
+    hipFunction_t f =
+        attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, nullptr, nullptr, 0);
     if (f) per_cu = std::min<uint32_t>(occupancy(rt, f, 0), 2);
     const uint32_t g = q_heads / kv_heads;
     if (kv_dtype == AMMON_BF16 && head == 128 && (g & (g - 1)) == 0) min_split = 64;
@@ -519,7 +527,8 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
   AMMON_CHECK(!overlaps(out, qbytes, q, qbytes) && !overlaps(out, qbytes, partial, need) &&
                   !overlaps(q, qbytes, partial, need),
               "attention_prefill: q, partial and out must not overlap");
-  hipFunction_t f = attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache);
+  hipFunction_t f =
+      attention_kernel(rt, kv_dtype, q_heads, kv_heads, head, k_cache, v_cache, split_len);
   AMMON_CHECK(f, "attention_prefill: head %u needs an even width above 64", head);
   VALIDATE_ONLY();
   // the partial layout and the grid cover ctx positions: [tokens][q_heads][splits][head + 2];
@@ -948,211 +957,6 @@ ammon_status ammon_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const 
   a.eps = eps;
   a.y = hb;
   return gemv_check_and_launch(rt, stream, a, "gate_up_swiglu");
-}
-
-// ---- one-launch blocks --------------------------------------------------------------------
-// A barrier wait gives up after this many polls (each sleeps ~64 clocks
-// and waits for a load: well over 0.1 s) and flags the launch.
-static uint32_t block_spin_limit() {
-  uint32_t limit = 200000;
-  if (const char *env = std::getenv("AMMON_BLOCK_SPIN_LIMIT")) {
-    const long v = std::atol(env);
-    if (v > 0) limit = (uint32_t)std::min<long>(v, 200000);
-  }
-  return limit;
-}
-
-static bool aligned16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
-
-// Resident workgroups for a barrier kernel: two per CU where the occupancy
-// allows (the grid every phase is tuned for), else one.
-static uint32_t block_grid(ammon_runtime *rt, hipFunction_t f, size_t lds) {
-  const uint32_t occ = occupancy(rt, f, lds);
-  return (uint32_t)std::max(rt->info.compute_units, 1) * std::min<uint32_t>(occ, 2);
-}
-
-ammon_status ammon_attention_block(ammon_runtime *rt, ammon_stream stream, float *x,
-                                   const void *norm_weight, ammon_dtype norm_dtype, float eps,
-                                   const void *wq, const void *wk, const void *wv, const void *wo,
-                                   ammon_dtype w_dtype, uint32_t dim, uint32_t q_heads,
-                                   uint32_t kv_heads, uint32_t head, void *k_cache, void *v_cache,
-                                   ammon_dtype kv_dtype, uint32_t seq,
-                                   const ammon_decode_step *step, const float *table,
-                                   uint32_t split_len, float *q, float *att, float *partial,
-                                   size_t partial_bytes, uint32_t *sync) {
-  REQUIRE_RT();
-  const char *what = "attention_block";
-  AMMON_CHECK(x && wo && q && att && partial && sync, "%s: NULL x, wo, q, att, partial or sync",
-              what);
-  AMMON_CHECK(w_dtype == AMMON_BF16 && kv_dtype == AMMON_BF16,
-              "%s: one launch needs bf16 weights and a bf16 KV cache", what);
-  AMMON_CHECK(head == 128, "%s: one launch needs head 128, got %u", what, head);
-  const uint32_t g = kv_heads ? q_heads / kv_heads : 0;
-  AMMON_CHECK(kv_heads > 0 && q_heads % kv_heads == 0 && (g == 1 || g == 2 || g == 4),
-              "%s: one launch needs 1, 2 or 4 q heads per kv head", what);
-  AMMON_CHECK(dim % 8 == 0 && aligned16(wq) && aligned16(wk) && aligned16(wv) && aligned16(wo) &&
-                  aligned16(x) && aligned16(q) && aligned16(att),
-              "%s: x, q, att and the weights must be 16-byte aligned with dim a multiple of 8",
-              what);
-  // the launch list's contract, with its own messages
-  ammon_status st =
-      ammon_qkv_rope_store(rt, AMMON_STREAM_VALIDATE, x, norm_weight, norm_dtype, eps, wq, wk, wv,
-                           w_dtype, dim, q_heads, kv_heads, head, q, k_cache, v_cache, kv_dtype,
-                           seq, step, table);
-  if (st != AMMON_OK) return st;
-  st = ammon_attention_decode(rt, AMMON_STREAM_VALIDATE, q, q_heads, k_cache, v_cache, kv_dtype,
-                              kv_heads, head, seq, step, split_len, partial, partial_bytes, att);
-  if (st != AMMON_OK) return st;
-  const uint32_t q_dim = q_heads * head, kv_dim = kv_heads * head;
-  st = ammon_gemv(rt, AMMON_STREAM_VALIDATE, wo, w_dtype, dim, q_dim, att, x, x);
-  if (st != AMMON_OK) return st;
-  const size_t qb = (size_t)q_dim * 4, pb = partial_bytes, sb = AMMON_BLOCK_SYNC_WORDS * 4;
-  AMMON_CHECK(!overlaps(q, qb, att, qb) && !overlaps(partial, pb, q, qb) &&
-                  !overlaps(partial, pb, att, qb) && !overlaps(sync, sb, q, qb) &&
-                  !overlaps(sync, sb, att, qb) && !overlaps(sync, sb, partial, pb) &&
-                  !overlaps(sync, sb, x, (size_t)dim * 4),
-              "%s: q, att, partial and sync must not overlap each other or x", what);
-
-  ammon_k_attn_block p = {};
-  GemvArgs a = {};
-  a.mode = AMMON_GEMV_QKV;
-  a.w0 = wq;
-  a.w1 = wk;
-  a.w2 = wv;
-  a.w_dtype = w_dtype;
-  a.d = q_dim;
-  a.n = dim;
-  a.rows = q_dim + 2 * kv_dim;
-  a.x = x;
-  a.norm_w = norm_weight;
-  a.norm_dtype = norm_dtype;
-  a.eps = eps;
-  a.y = q;
-  a.k_cache = k_cache;
-  a.v_cache = v_cache;
-  a.step = step;
-  a.table = table;
-  a.kv_dim = kv_dim;
-  a.head = head;
-  a.seq = seq;
-  a.kv_dtype = kv_dtype;
-  size_t lds_qkv = 0, lds_wo = 0;
-  int vec_qkv = 0, vec_wo = 0;
-  st = gemv_pack(rt, a, what, &p.qkv, &lds_qkv, &vec_qkv);
-  if (st != AMMON_OK) return st;
-  GemvArgs b = {};
-  b.mode = AMMON_GEMV_RESIDUAL;
-  b.w0 = wo;
-  b.w_dtype = w_dtype;
-  b.d = dim;
-  b.n = q_dim;
-  b.rows = dim;
-  b.x = att;
-  b.residual = x;
-  b.y = x;
-  st = gemv_pack(rt, b, what, &p.wo, &lds_wo, &vec_wo);
-  if (st != AMMON_OK) return st;
-  AMMON_CHECK(vec_qkv && vec_wo, "%s: rows must be whole 16-byte chunks", what);
-  const uint32_t splits = ammon_attention_splits(seq, split_len);
-  p.att = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, att,
-           q_heads, kv_heads, head, seq, split_len, splits, 0, seq, 0};
-  p.sync = sync;
-  p.spin_limit = block_spin_limit();
-  VALIDATE_ONLY();
-  hipFunction_t fn = rt->k.attn_block[att_group_index(g)];
-  AMMON_CHECK(fn != nullptr, "%s: kernel not loaded", what);
-  // LDS: x staged for either GEMV, a split-K unit's merge, or a merge unit
-  const size_t att_lds = ((size_t)kWorkgroup * (g * 8 + 1) + (size_t)kWorkgroup * g) * 4;
-  const size_t comb_lds = (64 * 9 + 64 + kWaves) * 4;
-  const size_t lds = std::max(std::max(lds_qkv, lds_wo), std::max(att_lds, comb_lds));
-  const uint32_t grid = block_grid(rt, fn, lds);
-  AMMON_CHECK(grid >= 8, "%s: %u resident workgroups are too few for the grid barrier", what,
-              grid);
-  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
-}
-
-ammon_status ammon_swiglu_block(ammon_runtime *rt, ammon_stream stream, float *x,
-                                const void *norm_weight, ammon_dtype norm_dtype, float eps,
-                                const void *w1, const void *w3, const void *w2,
-                                ammon_dtype w_dtype, uint32_t dim, uint32_t hidden, float *hb,
-                                uint32_t *sync) {
-  REQUIRE_RT();
-  const char *what = "swiglu_block";
-  AMMON_CHECK(x && w2 && hb && sync, "%s: NULL x, w2, hb or sync", what);
-  AMMON_CHECK(w_dtype == AMMON_BF16, "%s: one launch needs bf16 weights", what);
-  AMMON_CHECK(dim % 8 == 0 && hidden % 8 == 0 && aligned16(w1) && aligned16(w3) &&
-                  aligned16(w2) && aligned16(x) && aligned16(hb),
-              "%s: x, hb and the weights must be 16-byte aligned with dim and hidden multiples "
-              "of 8",
-              what);
-  ammon_status st = ammon_gate_up_swiglu(rt, AMMON_STREAM_VALIDATE, x, norm_weight, norm_dtype,
-                                         eps, w1, w3, w_dtype, dim, hidden, hb);
-  if (st != AMMON_OK) return st;
-  st = ammon_gemv(rt, AMMON_STREAM_VALIDATE, w2, w_dtype, dim, hidden, hb, x, x);
-  if (st != AMMON_OK) return st;
-  const size_t sb = AMMON_BLOCK_SYNC_WORDS * 4;
-  AMMON_CHECK(!overlaps(sync, sb, hb, (size_t)hidden * 4) &&
-                  !overlaps(sync, sb, x, (size_t)dim * 4),
-              "%s: sync must not overlap x or hb", what);
-
-  ammon_k_ffn_block p = {};
-  GemvArgs a = {};
-  a.mode = AMMON_GEMV_SWIGLU;
-  a.w0 = w1;
-  a.w1 = w3;
-  a.w_dtype = w_dtype;
-  a.d = hidden;
-  a.n = dim;
-  a.rows = 2 * hidden;
-  a.x = x;
-  a.norm_w = norm_weight;
-  a.norm_dtype = norm_dtype;
-  a.eps = eps;
-  a.y = hb;
-  size_t lds_gu = 0, lds_down = 0;
-  int vec_gu = 0, vec_down = 0;
-  st = gemv_pack(rt, a, what, &p.gate_up, &lds_gu, &vec_gu);
-  if (st != AMMON_OK) return st;
-  GemvArgs b = {};
-  b.mode = AMMON_GEMV_RESIDUAL;
-  b.w0 = w2;
-  b.w_dtype = w_dtype;
-  b.d = dim;
-  b.n = hidden;
-  b.rows = dim;
-  b.x = hb;
-  b.residual = x;
-  b.y = x;
-  st = gemv_pack(rt, b, what, &p.down, &lds_down, &vec_down);
-  if (st != AMMON_OK) return st;
-  AMMON_CHECK(vec_gu && vec_down, "%s: rows must be whole 16-byte chunks", what);
-  p.sync = sync;
-  p.spin_limit = block_spin_limit();
-  VALIDATE_ONLY();
-  hipFunction_t fn = rt->k.ffn_block;
-  AMMON_CHECK(fn != nullptr, "%s: kernel not loaded", what);
-  const size_t lds = std::max(lds_gu, lds_down);
-  const uint32_t grid = block_grid(rt, fn, lds);
-  AMMON_CHECK(grid >= 8, "%s: %u resident workgroups are too few for the grid barrier", what,
-              grid);
-  return launch(rt, stream, fn, grid, 1, (uint32_t)lds, p, what);
-}
-
-ammon_status ammon_block_sync_check(ammon_runtime *rt, ammon_stream stream, uint32_t *sync) {
-  REQUIRE_RT();
-  AMMON_CHECK(sync != nullptr, "block_sync_check: NULL sync");
-  uint32_t err = 0;
-  ammon_status st = ammon_memcpy(rt, &err, sync + AMMON_BLOCK_SYNC_ERR, sizeof err,
-                                 AMMON_COPY_D2H, stream);
-  if (st == AMMON_OK) st = ammon_stream_synchronize(rt, stream);
-  if (st != AMMON_OK || err == 0) return st;
-  // the launch's results are invalid; clear the words for the next one
-  st = ammon_fill(rt, stream, sync, AMMON_F32, AMMON_BLOCK_SYNC_WORDS, 0.f);
-  if (st == AMMON_OK) st = ammon_stream_synchronize(rt, stream);
-  if (st != AMMON_OK) return st;
-  return set_error(AMMON_E_HIP,
-                   "a grid barrier of a one-launch block timed out (workgroups not co-resident); "
-                   "the results of that launch are invalid");
 }
 
 // ---- argmax ---------------------------------------------------------------------------------

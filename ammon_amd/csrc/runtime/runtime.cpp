@@ -27,9 +27,7 @@ AMMON_BLOB(rope)
 AMMON_BLOB(attention)
 AMMON_BLOB(gemv)
 AMMON_BLOB(misc)
-AMMON_BLOB(token)
 AMMON_BLOB(prefill)
-AMMON_BLOB(block)
 
 namespace ammon_rt {
 
@@ -82,8 +80,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   } blobs[] = {{"embed", ammon_co_embed}, {"norm", ammon_co_norm},
                {"rope", ammon_co_rope},   {"attention", ammon_co_attention},
                {"gemv", ammon_co_gemv},   {"misc", ammon_co_misc},
-               {"token", ammon_co_token}, {"prefill", ammon_co_prefill},
-               {"block", ammon_co_block}};
+               {"prefill", ammon_co_prefill}};
   constexpr int kModules = (int)(sizeof(blobs) / sizeof(blobs[0]));
   hipModule_t mods[kModules];
   for (int i = 0; i < kModules; ++i) {
@@ -114,12 +111,16 @@ static ammon_status load_kernels(ammon_runtime *rt) {
         R(3, name, k.att_partial[d][c][g]);
       }
     }
-  for (int d = 0; d < 2; ++d)
+  for (int g = 0; g < kAttGroups; ++g) {
+    char name[96];
+    snprintf(name, sizeof name, "ammon_attention_partial_h128_f32_c4_g%d", gs[g]);
+    R(3, name, k.att_partial_h128_f32[g]);
+  }
+  for (int b = 0; b < 2; ++b)
     for (int g = 0; g < kAttGroups; ++g) {
       char name[96];
-      snprintf(name, sizeof name, "ammon_attention_partial_h128_%s_g%d",
-               d ? "bf16_c8" : "f32_c4", gs[g]);
-      R(3, name, k.att_partial_h128[d][g]);
+      snprintf(name, sizeof name, "ammon_attention_partial_h128_bf16_lds%d_g%d", 1 << b, gs[g]);
+      R(3, name, k.att_partial_staged[b][g]);
     }
   const char *modes[kGemvModes] = {"plain", "residual", "swiglu", "qkv"};
   for (int d = 0; d < 2; ++d)
@@ -145,35 +146,23 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   R(5, "ammon_fill_const", k.fill_const);
   R(5, "ammon_checksum", k.checksum);
   for (int d = 0; d < 2; ++d)
-    for (int g = 0; g < kAttGroups; ++g) {
-      char name[96];
-      snprintf(name, sizeof name, "ammon_token_bf16_kv%s_g%d", dtn[d], gs[g]);
-      R(6, name, k.token[d][g]);
-    }
-  for (int d = 0; d < 2; ++d)
     for (int t = 0; t < 2; ++t)
       for (int s = 0; s < 2; ++s)
         for (int m = 0; m < kGemvModes; ++m) {
           char name[96];
           snprintf(name, sizeof name, "ammon_gemm_%s_%s_t%d%s", dtn[d], modes[m], t ? 32 : 16,
                    s ? "_k4" : "");
-          R(7, name, k.gemm[d][t][s][m]);
+          R(6, name, k.gemm[d][t][s][m]);
         }
-  R(7, "ammon_gemm_reduce", k.gemm_reduce);
-  R(7, "ammon_gemm_reduce_qkv", k.gemm_reduce_qkv);
-  for (int g = 0; g < 3; ++g) {
-    char name[96];
-    snprintf(name, sizeof name, "ammon_attn_block_bf16_g%d", gs[g]);
-    R(8, name, k.attn_block[g]);
-  }
-  R(8, "ammon_ffn_block_bf16", k.ffn_block);
+  R(6, "ammon_gemm_reduce", k.gemm_reduce);
+  R(6, "ammon_gemm_reduce_qkv", k.gemm_reduce_qkv);
   for (int t = 0; t < 2; ++t)
     for (int r = 0; r < 2; ++r)
       for (int m = 0; m < kGemvModes; ++m) {
         char name[96];
         snprintf(name, sizeof name, "ammon_gemm_bf16_%s_t%d_r%d", modes[m], t ? 32 : 64,
                  r ? 2 : 4);
-        R(7, name, k.gemm_big[t][r][m]);
+        R(6, name, k.gemm_big[t][r][m]);
       }
 #undef R
   return AMMON_OK;

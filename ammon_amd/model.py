@@ -95,15 +95,13 @@ class LlamaModel:
     """
 
     def __init__(self, rt: Runtime, cfg, weights: dict, use_graph: bool = True,
-                 split_len: int = 0, persistent: bool = False,
-                 one_launch_blocks: bool = False):
+                 split_len: int = 0):
         self.rt = rt
         self.cfg = cfg
         self.weights = weights  # keeps the device buffers alive
         c = _abi.LlamaConfig(cfg.dim, cfg.n_layers, cfg.n_heads, cfg.n_kv_heads, cfg.hidden,
                              cfg.vocab, cfg.max_seq, cfg.theta, cfg.eps, cfg.w_dtype,
-                             cfg.kv_dtype, int(use_graph), split_len, int(persistent),
-                             int(one_launch_blocks))
+                             cfg.kv_dtype, int(use_graph), split_len)
         w = _abi.LlamaWeights(*[ctypes.c_void_p(int(weights[n])) for n in WEIGHT_NAMES])
         h = ctypes.c_void_p()
         call("ammon_llama_create", rt.handle, ctypes.byref(c), ctypes.byref(w), ctypes.byref(h))
@@ -247,23 +245,6 @@ class LlamaModel:
         n = ctypes.c_uint32()
         call("ammon_llama_launches", self.handle, ctypes.byref(n))
         return n.value
-
-    def token_trace(self):
-        """Barrier stamps of the persistent kernel's latest token, or None
-        when tracing is off (AMMON_TOKEN_TRACE=1 at construction enables it):
-        uint64 [barriers, 2, workgroups] of 100 MHz device-clock ticks,
-        [b, 0, w] = arrival of workgroup w at barrier b, [b, 1, w] = end of
-        its wait.  Barriers: embed, 6 per layer (QKV, attention, merge, wo,
-        gate/up, down), LM head, argmax."""
-        slots, wgs = ctypes.c_uint32(), ctypes.c_uint32()
-        call("ammon_llama_token_trace", self.handle, None, 0, ctypes.byref(slots),
-             ctypes.byref(wgs))
-        if slots.value == 0:
-            return None
-        buf = np.zeros(2 * slots.value * wgs.value, dtype=np.uint64)
-        call("ammon_llama_token_trace", self.handle, buf.ctypes.data_as(ctypes.c_void_p), buf.size,
-             ctypes.byref(slots), ctypes.byref(wgs))
-        return buf.reshape(slots.value, 2, wgs.value)
 
     def synchronize(self) -> None:
         self.rt.synchronize(self.stream)

@@ -64,11 +64,6 @@ def kernel_bytes(c, ctx, split=128):
         # the merge reads each live split's (acc, m, l) once and writes out
         "attention_combine": c.n_heads * -(-ctx // split) * (head + 2) * 4 + 4 * q,
         "lm_head": c.vocab * c.dim * 2 + 4 * c.dim * 2 + 4 * c.vocab,
-        # one launch per block: the algorithmic bytes of its parts
-        "attention_block": ((q + 2 * kv) * c.dim * 2 + 4 * c.dim * 2 + 4 * q + 2 * 2 * kv)
-                           + (2 * ctx * kv * 2 + 8 * q) + (c.dim * q * 2 + 4 * q + 4 * c.dim * 2),
-        "swiglu_block": (2 * c.hidden * c.dim * 2 + 4 * c.dim * 2 + 4 * c.hidden)
-                        + (c.dim * c.hidden * 2 + 4 * c.hidden + 4 * c.dim * 2),
     }
 
 
@@ -97,10 +92,6 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
             rt.handle, c.n_heads, c.n_kv_heads, head, c.kv_dtype, c.max_seq))
     part_bytes = ammon_amd.attention_scratch_bytes(c.n_heads, head, c.max_seq, split)
     part = rt.alloc(part_bytes)
-    att = rt.alloc(q * 4)
-    syncs = [rt.alloc(4 * 640), rt.alloc(4 * 640)]  # barrier words of the one-launch blocks
-    for s in syncs:
-        rt.fill(s, F32, 640, 0.0)
     rt.synchronize()
 
     def w(name, l, per):
@@ -134,15 +125,6 @@ def time_kernels(rt, model, c, weights, ctx, reps, split=0, use_graph=True):
         "lm_head": ("ammon_gemv_rmsnorm", lambda l: (
             rt.handle, stream, x, weights["rms_final"], F32, c.eps, weights["wcls"], BF16,
             c.vocab, c.dim, logits)),
-        "attention_block": ("ammon_attention_block", lambda l: (
-            rt.handle, stream, xr, rms("rms_att", l), F32, c.eps, w("wq", l, q * c.dim),
-            w("wk", l, kv * c.dim), w("wv", l, kv * c.dim), w("wo", l, c.dim * q), BF16, c.dim,
-            c.n_heads, c.n_kv_heads, head, *kv_ptr(l), BF16, c.max_seq, step, table, split, qb,
-            att, part, part_bytes, syncs[0])),
-        "swiglu_block": ("ammon_swiglu_block", lambda l: (
-            rt.handle, stream, xr, rms("rms_ffn", l), F32, c.eps, w("w1", l, c.hidden * c.dim),
-            w("w3", l, c.hidden * c.dim), w("w2", l, c.dim * c.hidden), BF16, c.dim, c.hidden,
-            hb, syncs[1])),
     }
     out = {}
     nbytes = kernel_bytes(c, ctx, split)
@@ -738,8 +720,6 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="seconds of CPU decode for the baseline (0 skips it)")
     ap.add_argument("--no-graph", action="store_true", help="replay launches without a graph")
-    ap.add_argument("--persistent", action="store_true",
-                    help="one persistent cooperative kernel per token")
     ap.add_argument("--split", type=int, default=0,
                     help="attention split length (0: the library's choice)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prompt-prefill lines")
@@ -777,8 +757,7 @@ def main():
     log(f"device {rt.info.arch.decode()} cus={rt.info.compute_units}; generating weights")
     t0 = time.time()
     model = ammon_amd.LlamaModel.synthetic(rt, c, seed=2024, std=0.02,
-                                           use_graph=not args.no_graph, split_len=args.split,
-                                           persistent=args.persistent)
+                                           use_graph=not args.no_graph, split_len=args.split)
     head = c.dim // c.n_heads
     kv_n = c.n_kv_heads * c.max_seq * head
     for l in range(c.n_layers):
@@ -788,9 +767,8 @@ def main():
         rt.fill_normal(v, BF16, kv_n, 7, 2 * l + 1)
     rt.synchronize()
     # the decode graph: the step's launch list with the LM head carrying the
-    # argmax's first pass, plus the argmax's second pass (one launch when
-    # persistent)
-    launches = 1 if args.persistent else model.launches + 1
+    # argmax's first pass, plus the argmax's second pass
+    launches = model.launches + 1
     log(f"weights + KV prefill in {time.time() - t0:.1f}s; launches/token={launches}")
 
     if args.copy_probe:

@@ -311,49 +311,6 @@ ammon_status ammon_gate_up_swiglu(ammon_runtime *rt, ammon_stream stream, const 
                                   const void *w1, const void *w3, ammon_dtype w_dtype,
                                   uint32_t dim, uint32_t hidden, float *hb);
 
-/* ---- one-launch blocks ------------------------------------------------------
- * The reference records an attention block as rmsnorm, the q/k/v
- * projections, rope_store, cache_store, the split attention pair, the output
- * projection and a residual add (src/blocks.rs:172-259), and a SwiGLU block
- * as rmsnorm, the gate/up projections, swiglu, the down projection and a
- * residual add (src/blocks.rs:261-278).  These entry points run each block as
- * ONE launch whose workgroups hand results to each other through grid
- * barriers: the same per-row and per-unit arithmetic as the separate calls
- * above (bit-identical results) with fewer device-wide drains, and the next
- * phase's weights and K/V requested before each barrier.
- *
- * Shapes: bf16 weights, dims multiples of 8, 16-byte-aligned rows; the
- * attention block also a bf16 KV cache, head 128 and 1, 2 or 4 q heads per
- * kv head.  Other shapes return AMMON_E_VALIDATION (use the separate calls).
- * q [q_heads * head], att [q_heads * head], partial (as for
- * ammon_attention_decode) and hb [hidden] are the blocks' intermediates.
- *
- * `sync`: AMMON_BLOCK_SYNC_WORDS words of device memory, zeroed once before
- * the first launch (ammon_fill); every launch that completes leaves them
- * zeroed.  One launch at a time per sync buffer.  If the workgroups cannot
- * all be resident at once (the device shared with other work), a barrier
- * stops waiting after a bounded time: that launch's results are invalid and
- * ammon_block_sync_check reports it. */
-#define AMMON_BLOCK_SYNC_WORDS 640u
-#define AMMON_BLOCK_SYNC_ERR 576u /* word set when a barrier wait gave up */
-ammon_status ammon_attention_block(ammon_runtime *rt, ammon_stream stream, float *x,
-                                   const void *norm_weight, ammon_dtype norm_dtype, float eps,
-                                   const void *wq, const void *wk, const void *wv, const void *wo,
-                                   ammon_dtype w_dtype, uint32_t dim, uint32_t q_heads,
-                                   uint32_t kv_heads, uint32_t head, void *k_cache, void *v_cache,
-                                   ammon_dtype kv_dtype, uint32_t seq,
-                                   const ammon_decode_step *step, const float *table,
-                                   uint32_t split_len, float *q, float *att, float *partial,
-                                   size_t partial_bytes, uint32_t *sync);
-ammon_status ammon_swiglu_block(ammon_runtime *rt, ammon_stream stream, float *x,
-                                const void *norm_weight, ammon_dtype norm_dtype, float eps,
-                                const void *w1, const void *w3, const void *w2,
-                                ammon_dtype w_dtype, uint32_t dim, uint32_t hidden, float *hb,
-                                uint32_t *sync);
-/* Waits for `stream`, then AMMON_E_HIP if a launch over `sync` flagged a
- * barrier that gave up (the words are cleared for the next launch). */
-ammon_status ammon_block_sync_check(ammon_runtime *rt, ammon_stream stream, uint32_t *sync);
-
 /* sample_argmax (reference src/tokenizer.rs:179-189) on device: first index
  * of the maximum, NaN never wins, NaN logits[0] gives 0.  `scratch` holds
  * ammon_argmax_scratch_bytes(n) bytes. */

@@ -324,14 +324,13 @@ struct AttentionOptions {
   float theta = AMMON_DEFAULT_ROPE_THETA;  // reference hard-wires 10000 (src/blocks.rs:234)
   float eps = 1e-5f;                       // reference literal (src/kernels.rs:94)
   uint32_t split_len = 0;                  // 0: pick per device and cache shape
-  bool one_launch = false;                 // ammon_attention_block where the shape allows
 };
 
 // Pre-norm causal attention block (src/modules.rs:189-274): RMSNorm, QKV,
 // RoPE, attention, output projection, residual into x.  Recorded as four
 // launches: norm+QKV+RoPE+KV store, split attention, LSE merge, wo +
-// residual; with one_launch, as one (ammon_attention_block) where its shape
-// contract holds.  Results are bit-identical either way.
+// residual (three when one split covers the cache: the attention pass then
+// writes the merged output).
 class CausalAttentionBlock {
  public:
   CausalAttentionBlock(const Runtime &rt, uint32_t hidden, uint32_t query_heads, uint32_t seq_len,
@@ -343,38 +342,30 @@ class CausalAttentionBlock {
                     const Tensor &step) const;
   // The split length record() uses for a cache of kv_heads heads in kv_dtype.
   uint32_t split_len_for(uint32_t kv_heads, DType kv_dtype) const;
-  // After the stream has drained: throws if a one-launch block recorded by
-  // this module flagged a grid barrier that stopped waiting.
-  void check(ammon_stream stream) const;
 
  private:
   Runtime rt_;
   uint32_t hidden_, q_heads_, head_, seq_;
   AttentionOptions opts_;
-  Tensor xb_, q_, partial_, sync_;
+  Tensor xb_, q_, partial_;
   std::shared_ptr<Tensor> table_;
   uint32_t max_splits_;
 };
 
 // Pre-norm SwiGLU block (src/modules.rs:276-333): RMSNorm, gated MLP,
-// residual.  Recorded as two launches: norm+gate/up+SwiGLU, down + residual;
-// with one_launch, as one (ammon_swiglu_block) where its shape contract
-// holds.  Results are bit-identical either way.
+// residual.  Recorded as two launches: norm+gate/up+SwiGLU, down + residual.
 class SwiGluBlock {
  public:
-  SwiGluBlock(const Runtime &rt, uint32_t hidden, uint32_t intermediate, float eps = 1e-5f,
-              bool one_launch = false);
+  SwiGluBlock(const Runtime &rt, uint32_t hidden, uint32_t intermediate, float eps = 1e-5f);
   void record(Scheme &s, TensorView x, const SwiGluBlockWeights &w) const;
   void record_group(Scheme &s, const std::string &label, TensorView x,
                     const SwiGluBlockWeights &w) const;
-  void check(ammon_stream stream) const;  // as CausalAttentionBlock::check
 
  private:
   Runtime rt_;
   uint32_t hidden_, inter_;
   float eps_;
-  bool one_launch_;
-  Tensor hb_, sync_;
+  Tensor hb_;
 };
 
 // ---- model contract and greedy loop ------------------------------------------------------

@@ -32,7 +32,7 @@ typedef struct ammon_checkpoint ammon_checkpoint;
 
 /* Read and validate the header only (host, no device): the model shape in
  * cfg (theta 10000 and eps 1e-5, llama2.c's; w_dtype / kv_dtype fp32;
- * use_graph 1; split_len 0; persistent 0), the layout, whether the
+ * use_graph 1; split_len 0), the layout, whether the
  * classifier is the embedding table, and the file size the shape implies. */
 ammon_status ammon_checkpoint_probe(const char *path, ammon_llama_config *cfg, uint32_t *format,
                                     uint32_t *shared_classifier, uint64_t *expected_bytes);

@@ -29,17 +29,9 @@ typedef struct ammon_llama_config {
   ammon_dtype w_dtype;  /* embedding table and projection matrices */
   ammon_dtype kv_dtype; /* KV cache storage */
   uint32_t use_graph;   /* replay each token as a captured HIP graph */
-  uint32_t split_len;   /* attention split length; 0 picks one (about two
-                           units per CU for the launch list, one per
-                           workgroup of the persistent kernel) */
-  uint32_t persistent;  /* run each token as one persistent cooperative kernel
-                           (bf16 weights, head 128, q heads per kv head in
-                           {1, 2, 4, 8}); other shapes use the launch list */
-  uint32_t one_launch_blocks; /* 1: record each attention / SwiGLU block as one
-                                 launch (ammon_attention_block,
-                                 ammon_swiglu_block) where the shape allows;
-                                 same results as the separate launches, which
-                                 measured faster on MI355X (the default) */
+  uint32_t split_len;   /* attention split length; 0 picks one sized to the
+                           device and the shape's kernel
+                           (ammon_attention_default_split_for) */
 } ammon_llama_config;
 
 typedef struct ammon_llama_weights {
@@ -121,19 +113,8 @@ ammon_status ammon_llama_tokens(ammon_llama *m, uint32_t start, uint32_t n, int3
 ammon_status ammon_llama_kv_layer(ammon_llama *m, uint32_t layer, void **key, void **value);
 ammon_status ammon_llama_stream(ammon_llama *m, ammon_stream *stream);
 ammon_status ammon_llama_logits(ammon_llama *m, float **device_logits);
-/* Number of kernel launches per token (greedy step excluded): 1 when the
- * persistent token kernel runs the model. */
+/* Number of kernel launches per token (greedy step excluded). */
 ammon_status ammon_llama_launches(ammon_llama *m, uint32_t *n);
-/* Barrier timestamps of the persistent token kernel's latest launch, for
- * phase timing (no counterpart in the reference, which has no persistent
- * kernel).  Recorded only when AMMON_TOKEN_TRACE=1 was set in the
- * environment when the model was created; otherwise *slots = 0.  Layout:
- * barrier b of slots (embed, 6 per layer, LM head, argmax), workgroup w of
- * *workgroups: host[2 b W + w] = arrival, host[(2 b + 1) W + w] = end of its
- * wait, in ticks of a 100 MHz device clock.  Copies at most `capacity` words
- * and waits for the model's stream. */
-ammon_status ammon_llama_token_trace(ammon_llama *m, uint64_t *host, size_t capacity,
-                                     uint32_t *slots, uint32_t *workgroups);
 
 #ifdef __cplusplus
 }

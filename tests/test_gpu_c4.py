@@ -16,9 +16,7 @@ names the first differing step and the oracle's top-2 logit margin there,
 so a near tie can be told apart from a bug.  The last step's logits: the
 two sides differ only in fp32 summation order (~4e-6 relative per
 projection), compounded over 32 layers and 527 steps of cache: within 1e-4
-normwise relative.  The same holds for the launch list's device and host
-loops and for the opt-in persistent decode-token kernel (one launch per
-token, its own attention split).
+normwise relative.  The same holds for the device and the host loop.
 """
 import json
 import os
@@ -115,25 +113,3 @@ def test_c4_host_greedy_tokens_match_oracle(c4):
     err = rel_err(logits, f["logits"])
     print(f"c4 host loop: last-step logits rel err {err:.2e}", flush=True)
     assert err <= DEEP_FP32_TOL
-
-
-def test_c4_persistent_kernel_greedy_tokens_match_oracle(c4, rt):
-    """The opt-in persistent decode-token kernel (one cooperative launch per
-    token, its own split length) on the same weights: tokens identical to
-    the oracle's, last logits within the same bar."""
-    model, f = c4
-    c = json.loads(str(f["config"]))
-    cfg = Cfg(**c, w_dtype=int(f["w_dtype"]), kv_dtype=int(f["kv_dtype"]))
-    fused = LlamaModel(rt, cfg, model.weights, persistent=True)
-    try:
-        assert fused.launches == 1
-        t0 = time.time()
-        toks, logits, tps = fused.generate_tokens_device(f["prompt"], int(f["max_new_tokens"]))
-        print(f"c4 persistent kernel: {len(toks)} tokens in {time.time() - t0:.1f} s "
-              f"({tps:.1f} tok/s)", flush=True)
-        check_tokens(toks, f)
-        err = rel_err(logits, f["logits"])
-        print(f"c4 persistent kernel: last-step logits rel err {err:.2e}", flush=True)
-        assert err <= DEEP_FP32_TOL
-    finally:
-        fused.close()

@@ -353,21 +353,45 @@ def test_default_split_sizes_units_to_kernel_occupancy(rt):
 
 @pytest.mark.parametrize("ctx", [1024, 4096, 8192])
 @pytest.mark.parametrize("kv_dtype", [BF16, F32])
-def test_attention_c3(rt, ctx, kv_dtype):
+@pytest.mark.parametrize("cache", ["seq8192", "seq_ctx"])
+def test_attention_c3(rt, ctx, kv_dtype, cache):
+    """Single-layer decode attention at the Llama-3-8B head shape, position
+    ctx - 1.  "seq8192": a cache sized 8192 at the kv-head-count split;
+    "seq_ctx": a cache of exactly ctx positions at the split the library
+    picks for the shape (ammon_attention_default_split_for: 64 at 1024 and
+    4096 positions for the bf16 matrix-core kernel, one 64-position chunk
+    per unit), as the decode attention of a ctx-sized cache runs it.  The
+    other positions of each split are checked too: the split's first,
+    a ragged last split, and a split boundary."""
     q_heads, kv_heads, head = 32, 8, 128
-    seq = 8192
+    seq = 8192 if cache == "seq8192" else ctx
     qh = oracle.normal(q_heads * head, 31).reshape(q_heads, head)
     kh = oracle.storage(oracle.normal(seq * kv_heads * head, 32), kv_dtype).reshape(
         seq, kv_heads, head)
     vh = oracle.storage(oracle.normal(seq * kv_heads * head, 33), kv_dtype).reshape(
         seq, kv_heads, head)
-    split = int(_abi.lib.ammon_attention_default_split(rt.handle, kv_heads, seq))
-    got, _ = run_attention(rt, qh, kh, vh, kv_dtype, q_heads, kv_heads, head, seq, ctx - 1, split)
-    want = oracle.attention(qh, kh, vh, kv_dtype, ctx - 1)
-    assert rel_err(got, want) <= RTOL
-    f64 = cpu_attention_f64(qh, oracle.widen(kh, kv_dtype), oracle.widen(vh, kv_dtype), q_heads,
-                            kv_heads, head, ctx - 1)
-    assert rel_err(got, f64) <= RTOL
+    if cache == "seq8192":
+        split = int(_abi.lib.ammon_attention_default_split(rt.handle, kv_heads, seq))
+        positions = [ctx - 1]
+    else:
+        split = int(_abi.lib.ammon_attention_default_split_for(rt.handle, q_heads, kv_heads, head,
+                                                                kv_dtype, seq))
+        if kv_dtype == BF16 and ctx <= 4096:
+            assert split == 64, split
+        # the last position, a ragged last split, a split's first position
+        positions = [ctx - 1, ctx - 1 - split // 2, ctx - split]
+    for pos in positions:
+        got, part = run_attention(rt, qh, kh, vh, kv_dtype, q_heads, kv_heads, head, seq, pos,
+                                  split)
+        want = oracle.attention(qh, kh, vh, kv_dtype, pos)
+        assert rel_err(got, want) <= RTOL, (pos, split)
+        f64 = cpu_attention_f64(qh, oracle.widen(kh, kv_dtype), oracle.widen(vh, kv_dtype),
+                                q_heads, kv_heads, head, pos)
+        assert rel_err(got, f64) <= RTOL, (pos, split)
+        if part.shape[1] > 1:
+            live = pos // split + 1
+            assert np.all(np.isfinite(part[:, :live])), (pos, split)
+            assert np.all(np.isnan(part[:, live:])), "a dead split was written"
 
 
 def test_attention_gqa8_c5_shape(rt):
