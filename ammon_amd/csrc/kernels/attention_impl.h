@@ -307,14 +307,6 @@ struct AttnPartial {
   }
 };
 
-// s_waitcnt that waits until at most N vector-memory operations of this wave
-// are outstanding (expcnt and lgkmcnt left at their maxima; gfx9 encoding:
-// vmcnt bits 3:0 and 15:14).
-template <int N> AMMON_DEV void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
-}
-
 // Compiler-level ordering of LDS accesses between the lanes of one wave: the
 // wave's LDS operations execute in program order, so a value one lane writes
 // is visible to another lane's later read once the compiler keeps the two in

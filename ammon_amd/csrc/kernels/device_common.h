@@ -67,6 +67,15 @@ AMMON_DEV float load_elem(const void *base, uint32_t dtype, size_t i) {
   return ((const float *)base)[i];
 }
 
+// s_waitcnt that waits until at most N vector-memory operations of this wave
+// are outstanding (expcnt and lgkmcnt left at their maxima; gfx9 encoding:
+// vmcnt bits 3:0 and 15:14).  Loads complete in order, so this is how a
+// wave waits for the requests it issued before its last N.
+template <int N> AMMON_DEV void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x70 | 0xF00);
+}
+
 // ---- chunk loads -----------------------------------------------------------
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

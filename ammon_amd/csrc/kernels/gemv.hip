@@ -24,7 +24,7 @@
     p.d = d;                                                                            \
     p.kv_dim = kv_dim;                                                                  \
     GemvPass<WT, CH, RPW, U, MODE> pass;                                                \
-    pass.begin(p, blockIdx.x, nwg);                                                     \
+    pass.begin(p, blockIdx.x, nwg, xs4);                                                \
     pass.run(xs4, red);                                                                 \
   }
 

@@ -53,11 +53,20 @@ struct GemvPass {
   using C = Chunk<WT, CH>;
   using V = typename C::V;
 
+  // x staging (run()): up to XREG 16-byte chunks of x (and of the norm
+  // weight) per lane through registers; longer x without a norm by 16-byte
+  // buffer loads straight into LDS; anything else by a loop in run().
+  static constexpr int XREG = 4;
+  enum XPath { X_REG, X_DMA, X_LOOP };
+
   ammon_k_gemv p;
   uint32_t wg, nwg;
   uint32_t n, tiles, wave_u, row_bytes;
   uint32_t blk, ti, blk1, ti1;
+  XPath xpath;
   float pre_a[RPW], pre_b[RPW];
+  float4 xr[XREG], wr[XREG];  // x and the fp32 norm weight (X_REG)
+  uint2 wb[XREG];             // ... or the bf16 norm weight's raw bits
   V bufA[RPW][U], bufB[RPW][U];
 
   static constexpr uint32_t tile_chunks = 64 * U;
@@ -133,9 +142,67 @@ struct GemvPass {
     }
   }
 
-  // Request the first two tiles of workgroup wg_ of nwg_.  Only weights are
-  // read, so this may run before x (or the residual / step) is final.
-  AMMON_DEV void begin(const ammon_k_gemv &params, uint32_t wg_, uint32_t nwg_) {
+  // LDS layout of x in 16-byte quads.  With 8-element chunks a lane needs
+  // two quads; they are stored as two planes of 64 quads per 64 chunks, so
+  // each ds_read_b128 of a wave covers 1 KiB of consecutive addresses
+  // (conflict-free) instead of a 32-byte lane stride.
+  AMMON_DEV static uint32_t xq(uint32_t q) {
+    if (CH == 8) return (q & ~127u) | ((q & 1u) << 6) | ((q >> 1) & 63u);
+    return q;
+  }
+
+  // Request x (and the norm weight) for staging: the registers of the
+  // X_REG path, or the buffer-to-LDS loads of the X_DMA path (wave w fills
+  // groups w, w + 4, ... of GQ quads: with 8-element chunks the two planes
+  // of a group are two loads, even quads then odd, each lane's 16 bytes
+  // landing at slot `lane` of its plane; quads past n read as zero).
+  AMMON_DEV void request_x(float4 *xs4) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const bool xvec = (n & 3u) == 0 && (((uintptr_t)p.x) & 15u) == 0;
+    // norm weights read four at a time: 8-byte (bf16) or 16-byte (fp32) loads
+    const bool wvec = p.norm_w == nullptr ||
+                      (((uintptr_t)p.norm_w) & (p.norm_dtype == AMMON_K_BF16 ? 7u : 15u)) == 0;
+    if (!p.norm_w && xvec && n / 4 > XREG * AMMON_WG) {
+      xpath = X_DMA;
+      const __amdgpu_buffer_rsrc_t xres = make_rsrc(p.x, n * 4u);
+      constexpr uint32_t GQ = CH == 8 ? 128 : 64;
+      static_assert(tile_chunks * CH / 4 % GQ == 0, "whole groups per tile");
+      const uint32_t groups = tiles * tile_chunks * CH / 4 / GQ;
+      for (uint32_t g = wave_u; g < groups; g += AMMON_WAVES) {
+#pragma unroll
+        for (uint32_t pl = 0; pl < GQ / 64; ++pl) {
+          const uint32_t q = g * GQ + (GQ == 128 ? 2 * lane + pl : lane);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(
+              xres, (__attribute__((address_space(3))) void *)(xs4 + g * GQ + pl * 64), 16,
+              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, 0);
+        }
+      }
+    } else if (xvec && wvec && n / 4 <= XREG * AMMON_WG) {
+      xpath = X_REG;
+#pragma unroll
+      for (int i = 0; i < XREG; ++i) {
+        const uint32_t c = tid + i * AMMON_WG;
+        if (c < n / 4) {
+          xr[i] = ld_in4(p.x + 4 * c);
+          // raw loads only (widened in run()): nothing here waits for a load
+          if (p.norm_w) {
+            if (p.norm_dtype == AMMON_K_BF16)
+              wb[i] = ((const uint2 *)p.norm_w)[c];
+            else
+              wr[i] = ((const float4 *)p.norm_w)[c];
+          }
+        }
+      }
+    } else {
+      xpath = X_LOOP;
+    }
+  }
+
+  // Request x (into registers or LDS) and then the first two tiles of
+  // workgroup wg_ of nwg_.  x first: it is small and shared by every
+  // workgroup, so it arrives ahead of the weights and its staging (and the
+  // norm) runs while the weights stream in.
+  AMMON_DEV void begin(const ammon_k_gemv &params, uint32_t wg_, uint32_t nwg_, float4 *xs4) {
     p = params;
     wg = wg_;
     nwg = nwg_;
@@ -149,6 +216,7 @@ struct GemvPass {
     blk1 = blk;
     ti1 = ti;
     advance(blk1, ti1, tiles, nwg);
+    request_x(xs4);
     load_tile(blk, ti, bufA);
     load_tile(blk1, ti1, bufB);
   }
@@ -167,66 +235,19 @@ struct GemvPass {
     if (MODE == AMMON_GEMV_QKV) pos = p.step->position;
     epi_load(wg, pos, pre_a, pre_b);
 
-    // LDS layout of x in 16-byte quads.  With 8-element chunks a lane needs
-    // two quads; they are stored as two planes of 64 quads per 64 chunks, so
-    // each ds_read_b128 of a wave covers 1 KiB of consecutive addresses
-    // (conflict-free) instead of a 32-byte lane stride.
-    auto xq = [](uint32_t q) -> uint32_t {
-      if (CH == 8) return (q & ~127u) | ((q & 1u) << 6) | ((q >> 1) & 63u);
-      return q;
-    };
     auto xi = [&](uint32_t j) -> uint32_t { return xq(j >> 2) * 4 + (j & 3u); };
 
     // ---- stage x, optional RMSNorm prologue ------------------------------
-    // Up to XREG 16-byte chunks of x (and of the norm weight) per lane go
-    // through registers: both loads issue together, the sum of squares and
-    // the normalisation need no extra LDS pass.  Longer rows take the LDS
-    // loop.
-    constexpr int XREG = 4;
+    // x was requested in begin(), ahead of the weight tiles.
     const bool xvec = (n & 3u) == 0 && (((uintptr_t)p.x) & 15u) == 0;
-    // norm weights read four at a time: 8-byte (bf16) or 16-byte (fp32) loads
     const bool wvec = p.norm_w == nullptr ||
                       (((uintptr_t)p.norm_w) & (p.norm_dtype == AMMON_K_BF16 ? 7u : 15u)) == 0;
-    if (!p.norm_w && xvec && n / 4 > XREG * AMMON_WG) {
-      // Long x without a norm (the down projection): 16-byte buffer loads
-      // straight into LDS, all of a wave's in flight at once and no
-      // registers held (the register loop below waits once per four
-      // quads); quads past n read as zero.  Wave w fills groups w, w + 4,
-      // ... of GQ quads: with 8-element chunks the two planes of a group
-      // are two loads (even quads, then odd), each lane's 16 bytes landing
-      // at slot lane of its plane.
-      const __amdgpu_buffer_rsrc_t xres = make_rsrc(p.x, n * 4u);
-      constexpr uint32_t GQ = CH == 8 ? 128 : 64;
-      static_assert(tile_chunks * CH / 4 % GQ == 0, "whole groups per tile");
-      const uint32_t groups = tiles * tile_chunks * CH / 4 / GQ;
-      for (uint32_t g = wave_u; g < groups; g += AMMON_WAVES) {
-#pragma unroll
-        for (uint32_t pl = 0; pl < GQ / 64; ++pl) {
-          const uint32_t q = g * GQ + (GQ == 128 ? 2 * lane + pl : lane);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(
-              xres, (__attribute__((address_space(3))) void *)(xs4 + g * GQ + pl * 64), 16,
-              q < n / 4 ? q * 16 : AMMON_OOB, 0, 0, 0);
-        }
-      }
-      __builtin_amdgcn_s_waitcnt(0);
-    } else if (xvec && wvec && n / 4 <= XREG * AMMON_WG) {
-      float4 xr[XREG], wr[XREG];
+    if (xpath == X_DMA) {
+      // this wave's x requests have landed: only the two tiles' requests
+      // (issued after them) may be outstanding
+      wait_vmcnt<2 * RPW * U>();
+    } else if (xpath == X_REG) {
       float ss = 0.f;
-#pragma unroll
-      for (int i = 0; i < XREG; ++i) {
-        const uint32_t c = tid + i * AMMON_WG;
-        if (c < n / 4) {
-          xr[i] = ld_in4(p.x + 4 * c);
-          if (p.norm_w) {
-            if (p.norm_dtype == AMMON_K_BF16) {
-              const uint2 wb = ((const uint2 *)p.norm_w)[c];
-              wr[i] = make_float4(bf16_lo(wb.x), bf16_hi(wb.x), bf16_lo(wb.y), bf16_hi(wb.y));
-            } else {
-              wr[i] = ((const float4 *)p.norm_w)[c];
-            }
-          }
-        }
-      }
 #pragma unroll
       for (int i = 0; i < XREG; ++i) {
         const uint32_t c = tid + i * AMMON_WG;
@@ -249,9 +270,14 @@ struct GemvPass {
         const uint32_t c = tid + i * AMMON_WG;
         if (c < n / 4) {
           float4 v = xr[i];
-          if (p.norm_w)
-            v = make_float4(wr[i].x * (s * v.x), wr[i].y * (s * v.y), wr[i].z * (s * v.z),
-                            wr[i].w * (s * v.w));
+          if (p.norm_w) {
+            const float4 w4 = p.norm_dtype == AMMON_K_BF16
+                                  ? make_float4(bf16_lo(wb[i].x), bf16_hi(wb[i].x),
+                                                bf16_lo(wb[i].y), bf16_hi(wb[i].y))
+                                  : wr[i];
+            v = make_float4(w4.x * (s * v.x), w4.y * (s * v.y), w4.z * (s * v.z),
+                            w4.w * (s * v.w));
+          }
           xs4[xq(c)] = v;
         }
       }

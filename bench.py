@@ -631,6 +631,87 @@ def c1_decode(rt, cpu_budget):
     return line
 
 
+C4_FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "tests", "golden",
+                          "c4_greedy.npz")
+
+
+def c4_generate(rt, cpu_budget):
+    """The Llama-3-8B-shaped greedy decode as configured: 32 layers, bf16
+    weights N(0, 0.02) (weight seed 1003), a seeded 16-token prompt and
+    max_new_tokens 528 -- 527 steps, 512 generated -- with tokens/s by the
+    reference's formula (src/generate.rs:73-84: steps after the first over
+    the time from the end of the first) for the device loop and the host
+    loop.  With the reference's fp32 cache the tokens are checked against
+    the oracle's run stored in tests/golden/c4_greedy.npz (all 527); with a
+    bf16 cache (the headline's storage) the same loops are timed.  CPU leg:
+    the oracle on the same weights from the same prompt for a bounded number
+    of steps, with token parity against the GPU's."""
+    import oracle
+    from ammon_amd import LlamaModel
+    from ammon_amd._abi import BF16, F32
+
+    f = np.load(C4_FIXTURE)
+    c4 = json.loads(str(f["config"]))
+    prompt = np.asarray(f["prompt"], np.int32)
+    max_new = int(f["max_new_tokens"])
+    want = np.asarray(f["tokens"], np.int32)
+    line = {"workload": "Llama-3-8B-shaped greedy decode, 16-token seeded prompt, "
+                        f"max_new_tokens {max_new} ({max_new - 1} steps, "
+                        f"{max_new - len(prompt)} generated); bf16 weights",
+            "steps": max_new - 1}
+    weights = None
+    for kv_name, kv in (("kv_f32", F32), ("kv_bf16", BF16)):
+        c = Cfg(**c4, w_dtype=BF16, kv_dtype=kv)
+        if weights is None:
+            m = LlamaModel.synthetic(rt, c, seed=int(f["weight_seed"]), std=0.02)
+            weights = m.weights
+        else:
+            m = LlamaModel(rt, c, weights)
+        m.generate_tokens_device(prompt, 16)  # warm: graph capture
+        toks, _, tps = m.generate_tokens_device(prompt, max_new)
+        toks_h, _, tps_h = m.generate_tokens(prompt, max_new)
+        r = {"tokens_per_s_device_loop": round(tps, 1), "tokens_per_s_host_loop": round(tps_h, 1),
+             "loops_agree": bool(np.array_equal(toks, toks_h))}
+        if kv == F32:
+            r["tokens_equal_oracle_fixture"] = bool(np.array_equal(toks, want) and
+                                                   np.array_equal(toks_h, want))
+            gpu_toks = toks
+        line[kv_name] = r
+        m.close()
+        log(f"C4 {kv_name}: {tps:.1f} tok/s device loop, {tps_h:.1f} host loop" +
+            (f"; tokens equal the oracle's fixture: {r['tokens_equal_oracle_fixture']}"
+             if kv == F32 else ""))
+    if cpu_budget > 0:
+        c = Cfg(**c4, w_dtype=BF16, kv_dtype=F32)
+        shapes = oracle.weight_shapes(oracle.LlamaConfig(**{k: c4[k] for k in (
+            "dim", "n_layers", "n_heads", "n_kv_heads", "hidden", "vocab", "max_seq")}))
+        host = {}
+        for name, buf in weights.items():
+            host[name] = buf.download(shapes[name],
+                                      np.float32 if name.startswith("rms") else np.uint16)
+        om = oracle.Model(oracle.LlamaConfig(**c4, w_dtype=BF16, kv_dtype=F32), host)
+        tok, toks, times = int(prompt[0]), [], []
+        for pos in range(max_new - 1):
+            t0 = time.perf_counter()
+            logits = om.step(tok, pos)
+            times.append(time.perf_counter() - t0)
+            tok = int(prompt[pos + 1]) if pos < len(prompt) - 1 else int(oracle.sample_argmax(logits))
+            toks.append(tok)
+            if sum(times) > cpu_budget:
+                break
+        om.close()
+        n = len(times)
+        line["cpu"] = {"tokens_per_s": round(n / sum(times), 2), "steps": n,
+                       "cores": oracle.num_threads(), "kind": "port",
+                       "sample": f"the first {n} of the {max_new - 1} steps, fp32 cache",
+                       "token_parity": bool(np.array_equal(toks, gpu_toks[:n]))}
+        log(f"C4 cpu: {line['cpu']['tokens_per_s']} tok/s over {n} steps; parity "
+            f"{line['cpu']['token_parity']}")
+    for buf in weights.values():
+        buf.free()
+    return line
+
+
 C5 = dict(dim=8192, n_layers=1, n_heads=64, n_kv_heads=8, hidden=28672, vocab=128256,
           max_seq=32768, theta=500000.0, eps=1e-5)
 
@@ -724,11 +805,11 @@ def main():
                     help="attention split length (0: the library's choice)")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prompt-prefill lines")
     ap.add_argument("--no-configs", action="store_true",
-                    help="skip the other workloads' lines (C1, C2, C3, C5) and the stream ceiling")
+                    help="skip the other workloads' lines (C1-C5) and the stream ceiling")
     ap.add_argument("--copy-probe", action="store_true",
                     help="also run a plain streaming kernel of known size (ammon_add over "
                          "256 MiB operands), the calibration for HBM byte counters")
-    ap.add_argument("--config", choices=("c1", "c5"),
+    ap.add_argument("--config", choices=("c1", "c2", "c3", "c4", "c5"),
                     help="run only that workload's line (no headline) and print it as JSON: "
                          "for profiling one workload on its own")
     args = ap.parse_args()
@@ -744,7 +825,24 @@ def main():
     if args.config:
         rt = Runtime(0)
         cb = 0.0 if args.no_cpu else args.cpu_budget
-        fn = {"c1": lambda: c1_decode(rt, cb), "c5": lambda: c5_layer(rt, min(cb, 10.0))}
+        if args.copy_probe:
+            copy_probe(rt)
+        small = 0.5 if cb > 0 else 0.0
+
+        def c2_alone():
+            from ammon_amd._abi import BF16
+            vocab, dim = LLAMA3_8B["vocab"], LLAMA3_8B["dim"]
+            table = rt.alloc(vocab * dim * 2)
+            rt.fill_normal(table, BF16, vocab * dim, 2024, 0, 0.0, 0.02)
+            try:
+                return c2_kernels(rt, None, table, small)
+            finally:
+                table.free()
+
+        fn = {"c1": lambda: c1_decode(rt, cb), "c2": c2_alone,
+              "c3": lambda: c3_attention(rt, None, small),
+              "c4": lambda: c4_generate(rt, min(cb, 10.0)),
+              "c5": lambda: c5_layer(rt, min(cb, 10.0))}
         print(json.dumps({"config": args.config, args.config: fn[args.config]()}), flush=True)
         return
 
@@ -822,6 +920,7 @@ def main():
                          ("c3", lambda: c3_attention(rt, stream, small)),
                          ("c2", lambda: c2_kernels(rt, stream, model.weights["tok_emb"], small)),
                          ("c1", lambda: c1_decode(rt, cb)),
+                         ("c4", lambda: c4_generate(rt, min(cb, 10.0))),
                          ("c5", lambda: c5_layer(rt, min(cb, 10.0)))):
             try:
                 extras[name] = fn()
@@ -872,7 +971,7 @@ def main():
         "prefill": prefill,
         "cpu_baseline": cpu,
         "stream_read_ceiling": extras.get("stream_read_ceiling"),
-        "configs": {k: extras[k] for k in ("c1", "c2", "c3", "c5") if k in extras},
+        "configs": {k: extras[k] for k in ("c1", "c2", "c3", "c4", "c5") if k in extras},
     }
     model.close()
     print(json.dumps(result), flush=True)

@@ -62,12 +62,17 @@ def _load() -> ctypes.CDLL:
         "orc_attention_serial": (None, [_P, _P, _P, ctypes.c_int, _U32, _U32, _U32, _U32, _U32, _P, _P]),
         "orc_swiglu": (None, [_P, _P, _U32]),
         "orc_gemv": (None, [_P, ctypes.c_int, _U32, _U32, _P, _P]),
+        "orc_gemv_scalar": (None, [_P, ctypes.c_int, _U32, _U32, _P, _P]),
+        "orc_set_gemv_order": (None, [ctypes.c_int]),
         "orc_add": (None, [_P, _P, _P, _U32]),
         "orc_sample_argmax": (_I32, [_P, _U32]),
         "orc_model_create": (_P, [_P, _P]),
         "orc_model_destroy": (None, [_P]),
         "orc_model_step": (None, [_P, _U32, _U32, _P]),
         "orc_model_key_cache": (_P, [_P, _U32]),
+        "orc_model_key_row": (_P, [_P, _U32]),
+        "orc_model_value_row": (_P, [_P, _U32]),
+        "orc_model_set_kv_store": (None, [_P, ctypes.c_int]),
         "orc_model_value_cache": (_P, [_P, _U32]),
         "orc_generate_tokens": (ctypes.c_int, [_P, _P, _U32, _U32, ctypes.c_int, _I32, _P, _P, _P]),
         "orc_num_threads": (ctypes.c_int, []),
@@ -225,6 +230,23 @@ def gemv(w: np.ndarray, w_dtype: int, x: np.ndarray) -> np.ndarray:
     return y
 
 
+def gemv_scalar(w: np.ndarray, w_dtype: int, x: np.ndarray) -> np.ndarray:
+    """gemv with one scalar chain per row (the check of the vector path)."""
+    d, n = w.shape
+    w = np.ascontiguousarray(w)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    y = np.empty(d, dtype=np.float32)
+    _lib.orc_gemv_scalar(_ptr(w), w_dtype, d, n, _ptr(x), _ptr(y))
+    return y
+
+
+def set_gemv_order(descending: bool) -> None:
+    """Every GEMV row summed with j descending (True) or ascending, the
+    reference's order (False, the default).  Process-wide; only for
+    measuring how far two valid summation orders drift apart."""
+    _lib.orc_set_gemv_order(int(bool(descending)))
+
+
 def add(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     a = np.ascontiguousarray(a, dtype=np.float32)
     b = np.ascontiguousarray(b, dtype=np.float32)
@@ -353,6 +375,39 @@ class Model:
             buf = (ctypes.c_char * (n * np.dtype(dt).itemsize)).from_address(p)
             out.append(np.frombuffer(buf, dtype=dt).reshape(shape).copy())
         return out[0], out[1]
+
+    def _kv_dtype(self):
+        return np.uint16 if self.config.kv_dtype == BF16 else np.float32
+
+    def kv_rows(self, layer: int):
+        """(key, value) rows [kv_heads, head] (storage arrays) that the
+        latest step computed for ``layer``, whether or not it stored them."""
+        c = self.config
+        dt = self._kv_dtype()
+        n = c.n_kv_heads * c.head
+        out = []
+        for fn in (_lib.orc_model_key_row, _lib.orc_model_value_row):
+            buf = (ctypes.c_char * (n * np.dtype(dt).itemsize)).from_address(fn(self._handle, layer))
+            out.append(np.frombuffer(buf, dtype=dt).reshape(c.n_kv_heads, c.head).copy())
+        return out[0], out[1]
+
+    def set_kv_store(self, on: bool) -> None:
+        """Whether steps store their K / V rows into the cache (the default)
+        or leave the cache as the caller wrote it (a test that writes the
+        position's rows itself)."""
+        _lib.orc_model_set_kv_store(self._handle, int(bool(on)))
+
+    def write_kv(self, layer: int, start: int, key: np.ndarray, value: np.ndarray) -> None:
+        """Write rows [n, kv_heads, head] (storage arrays in the cache dtype)
+        into ``layer``'s caches at positions start .. start + n."""
+        c = self.config
+        dt = self._kv_dtype()
+        row = c.n_kv_heads * c.head * np.dtype(dt).itemsize
+        for fn, a in ((_lib.orc_model_key_cache, key), (_lib.orc_model_value_cache, value)):
+            a = np.ascontiguousarray(a, dtype=dt).reshape(-1, c.n_kv_heads, c.head)
+            if start < 0 or start + a.shape[0] > c.max_seq:
+                raise ValueError("write_kv: rows outside the cache")
+            ctypes.memmove(fn(self._handle, layer) + start * row, a.ctypes.data, a.nbytes)
 
     def generate_tokens(self, prompt, max_new_tokens: int, stop_on=None):
         prompt = np.ascontiguousarray(prompt, dtype=np.int32)

@@ -167,12 +167,12 @@ void orc_rope_table(float theta, uint32_t head, uint32_t seq, float *table) {
 /* rope_store: reference src/kernels.rs:174-210.  Pair i = 2p over the whole
  * query width rotates q in place; pairs with i < kv_dim also write the
  * rotated key projection into K[pos] (position-major row of kv_dim). */
-void orc_rope_store(float *q, const float *k_proj, void *k_cache, int kv_dtype,
-                    uint32_t q_numel, uint32_t kv_dim, uint32_t head,
-                    uint32_t seq, uint32_t pos, const float *table) {
-  (void)seq;
+/* rope_store with the rotated k row written at k_row[0 .. kv_dim). */
+static void rope_store_row(float *q, const float *k_proj, void *k_row, int kv_dtype,
+                           uint32_t q_numel, uint32_t kv_dim, uint32_t head, uint32_t pos,
+                           const float *table) {
   const uint32_t half = head / 2;
-  const size_t k_base = (size_t)pos * kv_dim;
+  const size_t k_base = 0;
   for (uint32_t i = 0; i < q_numel; i += 2) {
     uint32_t hd = i % head;
     const float *cs = table + ((size_t)pos * half + hd / 2) * 2;
@@ -182,10 +182,18 @@ void orc_rope_store(float *q, const float *k_proj, void *k_cache, int kv_dtype,
     q[i + 1] = q0 * fci + q1 * fcr;
     if (i < kv_dim) {
       float k0 = k_proj[i], k1 = k_proj[i + 1];
-      store_elem(k_cache, kv_dtype, k_base + i, k0 * fcr - k1 * fci);
-      store_elem(k_cache, kv_dtype, k_base + i + 1, k0 * fci + k1 * fcr);
+      store_elem(k_row, kv_dtype, k_base + i, k0 * fcr - k1 * fci);
+      store_elem(k_row, kv_dtype, k_base + i + 1, k0 * fci + k1 * fcr);
     }
   }
+}
+
+void orc_rope_store(float *q, const float *k_proj, void *k_cache, int kv_dtype,
+                    uint32_t q_numel, uint32_t kv_dim, uint32_t head,
+                    uint32_t seq, uint32_t pos, const float *table) {
+  (void)seq;
+  rope_store_row(q, k_proj, (char *)k_cache + (size_t)pos * kv_dim * (kv_dtype == ORC_BF16 ? 2 : 4),
+                 kv_dtype, q_numel, kv_dim, head, pos, table);
 }
 
 /* cache_store: reference src/kernels.rs:212-226, V[pos * row + i] = v[i]. */
@@ -359,34 +367,156 @@ void orc_swiglu(float *hb, const float *hb2, uint32_t n) {
 }
 
 /* GEMV: the serial definition, reference src/kernels.rs:54-73
- * (y_i = sum_j W[i*n + j] x_j, j ascending).  Four rows are interleaved per
- * thread for instruction-level parallelism; each row's order is unchanged. */
+ * (y_i = sum_j W[i*n + j] x_j, j ascending).  Several rows are interleaved
+ * per thread for instruction-level parallelism; each row's order is
+ * unchanged. */
+
+/* Summation order of every GEMV row: 0 = the reference's (j ascending),
+ * 1 = j descending.  The descending order is not the reference's; it exists
+ * so a test can run the oracle against itself with one valid change of fp32
+ * summation order (how far two correct implementations drift apart). */
+static int g_gemv_order = 0;
+void orc_set_gemv_order(int descending) { g_gemv_order = descending ? 1 : 0; }
+
+/* Rows [r0, r0 + nr) (nr <= 4) of the serial gemv, j in the configured order. */
+static void gemv_rows_scalar(const void *w, int w_dtype, uint32_t r0, uint32_t nr, uint32_t n,
+                             const float *x, float *y) {
+  float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (uint32_t k = 0; k < n; ++k) {
+    const uint32_t j = g_gemv_order ? n - 1 - k : k;
+    const float xj = x[j];
+    for (uint32_t r = 0; r < nr; ++r) {
+      const size_t i = (size_t)(r0 + r) * n + j;
+      const float wv = w_dtype == ORC_BF16 ? orc_bf16_to_f32(((const uint16_t *)w)[i])
+                                           : ((const float *)w)[i];
+      s[r] = s[r] + wv * xj;
+    }
+  }
+  for (uint32_t r = 0; r < nr; ++r) y[r0 + r] = s[r];
+}
+
+#if defined(__x86_64__) && defined(__GNUC__)
+#include <immintrin.h>
+#define ORC_HAVE_AVX2_GEMV 1
+/* 32 rows [r0, r0 + 32) of the serial gemv with AVX2: each 8-float vector
+ * holds 8 rows' running sums, and every 8 x 8 block of W is transposed in
+ * registers so the sums advance one column at a time -- every row keeps the
+ * serial order (s = s + w_rj * x_j, j in the configured order, one rounding
+ * for the product and one for the sum), so the results equal the scalar
+ * loop's bit for bit.  Rows past d read row r0's data and are not stored.
+ * Columns past the last whole block of 8 run through the scalar tail, in
+ * order. */
+__attribute__((target("avx2"))) static void gemv_rows32_avx2(const void *w, int w_dtype,
+                                                             uint32_t r0, uint32_t d, uint32_t n,
+                                                             const float *x, float *y) {
+  const uint32_t n8 = n & ~7u;
+  const int desc = g_gemv_order;
+  __m256 acc[4];
+  size_t row[32];
+  for (int r = 0; r < 32; ++r) row[r] = (size_t)(r0 + r < d ? r0 + r : r0) * n;
+  for (int g = 0; g < 4; ++g) acc[g] = _mm256_setzero_ps();
+  /* descending: the tail columns come first, highest column first */
+  if (desc) {
+    for (uint32_t j = n; j-- > n8;) {
+      const float xj = x[j];
+      for (int g = 0; g < 4; ++g) {
+        float t[8];
+        _mm256_storeu_ps(t, acc[g]);
+        for (int r = 0; r < 8; ++r) {
+          const size_t i = row[8 * g + r] + j;
+          const float wv = w_dtype == ORC_BF16 ? orc_bf16_to_f32(((const uint16_t *)w)[i])
+                                               : ((const float *)w)[i];
+          t[r] = t[r] + wv * xj;
+        }
+        acc[g] = _mm256_loadu_ps(t);
+      }
+    }
+  }
+  for (uint32_t bi = 0; bi < n8 / 8; ++bi) {
+    const uint32_t j0 = desc ? n8 - 8 * (bi + 1) : 8 * bi;
+    __m256 xb[8];
+    for (int k = 0; k < 8; ++k) xb[k] = _mm256_set1_ps(x[j0 + k]);
+    for (int g = 0; g < 4; ++g) {
+      __m256 v[8];
+      for (int r = 0; r < 8; ++r) {
+        const size_t i = row[8 * g + r] + j0;
+        if (w_dtype == ORC_BF16) {
+          const __m128i h = _mm_loadu_si128((const __m128i *)((const uint16_t *)w + i));
+          v[r] = _mm256_castsi256_ps(_mm256_slli_epi32(_mm256_cvtepu16_epi32(h), 16));
+        } else {
+          v[r] = _mm256_loadu_ps((const float *)w + i);
+        }
+      }
+      /* 8 x 8 transpose: c[k] = (v[0][k], ..., v[7][k]) */
+      const __m256 t0 = _mm256_unpacklo_ps(v[0], v[1]), t1 = _mm256_unpackhi_ps(v[0], v[1]);
+      const __m256 t2 = _mm256_unpacklo_ps(v[2], v[3]), t3 = _mm256_unpackhi_ps(v[2], v[3]);
+      const __m256 t4 = _mm256_unpacklo_ps(v[4], v[5]), t5 = _mm256_unpackhi_ps(v[4], v[5]);
+      const __m256 t6 = _mm256_unpacklo_ps(v[6], v[7]), t7 = _mm256_unpackhi_ps(v[6], v[7]);
+      const __m256 u0 = _mm256_shuffle_ps(t0, t2, 0x44), u1 = _mm256_shuffle_ps(t0, t2, 0xEE);
+      const __m256 u2 = _mm256_shuffle_ps(t1, t3, 0x44), u3 = _mm256_shuffle_ps(t1, t3, 0xEE);
+      const __m256 u4 = _mm256_shuffle_ps(t4, t6, 0x44), u5 = _mm256_shuffle_ps(t4, t6, 0xEE);
+      const __m256 u6 = _mm256_shuffle_ps(t5, t7, 0x44), u7 = _mm256_shuffle_ps(t5, t7, 0xEE);
+      __m256 c[8];
+      c[0] = _mm256_permute2f128_ps(u0, u4, 0x20);
+      c[1] = _mm256_permute2f128_ps(u1, u5, 0x20);
+      c[2] = _mm256_permute2f128_ps(u2, u6, 0x20);
+      c[3] = _mm256_permute2f128_ps(u3, u7, 0x20);
+      c[4] = _mm256_permute2f128_ps(u0, u4, 0x31);
+      c[5] = _mm256_permute2f128_ps(u1, u5, 0x31);
+      c[6] = _mm256_permute2f128_ps(u2, u6, 0x31);
+      c[7] = _mm256_permute2f128_ps(u3, u7, 0x31);
+      __m256 a = acc[g];
+      if (desc) {
+        for (int k = 7; k >= 0; --k) a = _mm256_add_ps(a, _mm256_mul_ps(c[k], xb[k]));
+      } else {
+        for (int k = 0; k < 8; ++k) a = _mm256_add_ps(a, _mm256_mul_ps(c[k], xb[k]));
+      }
+      acc[g] = a;
+    }
+  }
+  float out[32];
+  for (int g = 0; g < 4; ++g) _mm256_storeu_ps(out + 8 * g, acc[g]);
+  if (!desc) {
+    for (uint32_t j = n8; j < n; ++j) {
+      const float xj = x[j];
+      for (int r = 0; r < 32; ++r) {
+        const size_t i = row[r] + j;
+        const float wv = w_dtype == ORC_BF16 ? orc_bf16_to_f32(((const uint16_t *)w)[i])
+                                             : ((const float *)w)[i];
+        out[r] = out[r] + wv * xj;
+      }
+    }
+  }
+  for (uint32_t r = 0; r < 32 && r0 + r < d; ++r) y[r0 + r] = out[r];
+}
+#endif
+
+/* gemv: reference serial definition src/kernels.rs:54-73,
+ * y_i = sum_j W[i*n + j] x_j accumulated in j order, one fp32 rounding per
+ * product and per sum.  OpenMP over blocks of output rows only. */
 void orc_gemv(const void *w, int w_dtype, uint32_t d, uint32_t n,
               const float *x, float *y) {
+#ifdef ORC_HAVE_AVX2_GEMV
+  if (__builtin_cpu_supports("avx2")) {
+    const int64_t blocks = ((int64_t)d + 31) / 32;
+#pragma omp parallel for schedule(static)
+    for (int64_t b = 0; b < blocks; ++b)
+      gemv_rows32_avx2(w, w_dtype, (uint32_t)b * 32, d, n, x, y);
+    return;
+  }
+#endif
+  orc_gemv_scalar(w, w_dtype, d, n, x, y);
+}
+
+/* The same, one scalar chain per row (the portable path, and the check of
+ * the vector path). */
+void orc_gemv_scalar(const void *w, int w_dtype, uint32_t d, uint32_t n,
+                     const float *x, float *y) {
   const int64_t blocks = ((int64_t)d + 3) / 4;
 #pragma omp parallel for schedule(static)
   for (int64_t b = 0; b < blocks; ++b) {
     const uint32_t r0 = (uint32_t)b * 4;
-    const uint32_t nr = (d - r0) < 4 ? (d - r0) : 4;
-    float s[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-    if (w_dtype == ORC_BF16) {
-      const uint16_t *wr[4];
-      for (uint32_t r = 0; r < 4; ++r)
-        wr[r] = (const uint16_t *)w + (size_t)(r0 + (r < nr ? r : 0)) * n;
-      for (uint32_t j = 0; j < n; ++j) {
-        const float xj = x[j];
-        for (uint32_t r = 0; r < 4; ++r) s[r] = s[r] + orc_bf16_to_f32(wr[r][j]) * xj;
-      }
-    } else {
-      const float *wr[4];
-      for (uint32_t r = 0; r < 4; ++r)
-        wr[r] = (const float *)w + (size_t)(r0 + (r < nr ? r : 0)) * n;
-      for (uint32_t j = 0; j < n; ++j) {
-        const float xj = x[j];
-        for (uint32_t r = 0; r < 4; ++r) s[r] = s[r] + wr[r][j] * xj;
-      }
-    }
-    for (uint32_t r = 0; r < nr; ++r) y[r0 + r] = s[r];
+    gemv_rows_scalar(w, w_dtype, r0, (d - r0) < 4 ? (d - r0) : 4, n, x, y);
   }
 }
 
@@ -419,6 +549,12 @@ struct orc_model {
   uint32_t head, q_dim, kv_dim, splits;
   float *x, *xb, *xb2, *q, *kp, *v, *hb, *hb2, *partial, *table;
   void *key, *value; /* [L, seq, kv_heads, head] */
+  /* The K / V rows the latest step computed, per layer [L, kv_dim] in the
+   * cache dtype, and whether a step stores them into the cache (1, the
+   * reference's behaviour) or leaves the cache untouched (0: a test has
+   * written the rows at the position itself). */
+  void *krow, *vrow;
+  int store_kv;
 };
 
 static size_t esize(int dtype) { return dtype == ORC_BF16 ? 2 : 4; }
@@ -445,6 +581,9 @@ orc_model *orc_model_create(const orc_config *cfg, const orc_weights *w) {
   size_t kv_elems = (size_t)cfg->n_layers * cfg->max_seq * m->kv_dim;
   m->key = calloc(kv_elems, esize(cfg->kv_dtype));
   m->value = calloc(kv_elems, esize(cfg->kv_dtype));
+  m->krow = calloc((size_t)cfg->n_layers * m->kv_dim, esize(cfg->kv_dtype));
+  m->vrow = calloc((size_t)cfg->n_layers * m->kv_dim, esize(cfg->kv_dtype));
+  m->store_kv = 1;
   return m;
 }
 
@@ -452,12 +591,22 @@ void orc_model_destroy(orc_model *m) {
   if (!m) return;
   free(m->x); free(m->xb); free(m->xb2); free(m->q); free(m->kp); free(m->v);
   free(m->hb); free(m->hb2); free(m->partial); free(m->table);
-  free(m->key); free(m->value);
+  free(m->key); free(m->value); free(m->krow); free(m->vrow);
   free(m);
 }
 
 static const void *layer_ptr(const void *base, int dtype, uint32_t l, size_t per_layer) {
   return (const char *)base + (size_t)l * per_layer * esize(dtype);
+}
+
+void orc_model_set_kv_store(orc_model *m, int on) { m->store_kv = on ? 1 : 0; }
+
+void *orc_model_key_row(orc_model *m, uint32_t layer) {
+  return (char *)m->krow + (size_t)layer * m->kv_dim * esize(m->c.kv_dtype);
+}
+
+void *orc_model_value_row(orc_model *m, uint32_t layer) {
+  return (char *)m->vrow + (size_t)layer * m->kv_dim * esize(m->c.kv_dtype);
 }
 
 void *orc_model_key_cache(orc_model *m, uint32_t layer) {
@@ -482,8 +631,17 @@ void orc_model_step(orc_model *m, uint32_t token, uint32_t pos, float *logits) {
     orc_gemv(layer_ptr(w->wq, wd, l, (size_t)m->q_dim * dim), wd, m->q_dim, dim, m->xb, m->q);
     orc_gemv(layer_ptr(w->wk, wd, l, (size_t)m->kv_dim * dim), wd, m->kv_dim, dim, m->xb, m->kp);
     orc_gemv(layer_ptr(w->wv, wd, l, (size_t)m->kv_dim * dim), wd, m->kv_dim, dim, m->xb, m->v);
-    orc_rope_store(m->q, m->kp, kc, c->kv_dtype, m->q_dim, m->kv_dim, m->head, c->max_seq, pos, m->table);
-    orc_cache_store(m->v, vc, c->kv_dtype, m->kv_dim, c->max_seq, pos);
+    /* rope_store + cache_store (src/blocks.rs:226-239): the rows in the
+     * cache dtype, then into the cache at pos */
+    const size_t row_bytes = (size_t)m->kv_dim * esize(c->kv_dtype);
+    char *krow = (char *)m->krow + (size_t)l * row_bytes;
+    char *vrow = (char *)m->vrow + (size_t)l * row_bytes;
+    rope_store_row(m->q, m->kp, krow, c->kv_dtype, m->q_dim, m->kv_dim, m->head, pos, m->table);
+    for (uint32_t i = 0; i < m->kv_dim; ++i) store_elem(vrow, c->kv_dtype, i, m->v[i]);
+    if (m->store_kv) {
+      memcpy((char *)kc + (size_t)pos * row_bytes, krow, row_bytes);
+      memcpy((char *)vc + (size_t)pos * row_bytes, vrow, row_bytes);
+    }
     orc_attention_partial(m->q, kc, vc, c->kv_dtype, c->n_heads, c->n_kv_heads, m->head,
                           c->max_seq, pos, m->partial);
     orc_attention_combine(m->partial, c->n_heads, m->head, c->max_seq, pos, m->xb);

@@ -68,6 +68,14 @@ void orc_attention_serial(const float *q, const void *k_cache,
 void orc_swiglu(float *hb, const float *hb2, uint32_t n);
 void orc_gemv(const void *w, int w_dtype, uint32_t d, uint32_t n,
               const float *x, float *y);
+/* The same with one scalar chain per row (no vector instructions): the
+ * check of the vector path, bit-identical to it. */
+void orc_gemv_scalar(const void *w, int w_dtype, uint32_t d, uint32_t n,
+                     const float *x, float *y);
+/* Summation order of every GEMV row: 0 (default) = the reference's, j
+ * ascending; 1 = j descending.  Only for measuring how far two valid
+ * summation orders drift apart; process-wide, not thread-safe. */
+void orc_set_gemv_order(int descending);
 void orc_add(const float *a, const float *b, float *out, uint32_t n);
 int32_t orc_sample_argmax(const float *logits, uint32_t n);
 
@@ -100,6 +108,12 @@ orc_model *orc_model_create(const orc_config *cfg, const orc_weights *w);
 void orc_model_destroy(orc_model *m);
 void orc_model_step(orc_model *m, uint32_t token, uint32_t pos, float *logits);
 /* Pointer to the layer-l key / value cache ([seq, kv_heads, head]). */
+/* Test hooks: the K / V rows (cache dtype, [kv_dim]) that the latest step
+ * computed for `layer`, and whether steps store them into the cache (1,
+ * the default, as the reference does) or leave it untouched (0). */
+void *orc_model_key_row(orc_model *m, uint32_t layer);
+void *orc_model_value_row(orc_model *m, uint32_t layer);
+void orc_model_set_kv_store(orc_model *m, int on);
 void *orc_model_key_cache(orc_model *m, uint32_t layer);
 void *orc_model_value_cache(orc_model *m, uint32_t layer);
 /* Greedy loop with the reference's semantics; returns 0 on success. */

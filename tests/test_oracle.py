@@ -229,6 +229,28 @@ def test_gemv_matches_f64_matmul(d, n, w_dtype):
     assert np.max(np.abs(got - want)) <= 1e-6 * np.sqrt(n) * np.max(np.abs(want)) + 1e-6
 
 
+@pytest.mark.parametrize("d,n", [(1, 1), (3, 7), (31, 9), (32, 8), (33, 17), (77, 1003),
+                                 (1024, 4096), (300, 14336)])
+@pytest.mark.parametrize("w_dtype", [F32, BF16])
+@pytest.mark.parametrize("descending", [False, True])
+def test_gemv_vector_path_equals_serial_chains(d, n, w_dtype, descending):
+    # The vector path (8 rows per register, 8 x 8 transposes) keeps every
+    # row's serial order: bit-identical to one scalar chain per row, in the
+    # reference's order and in the descending order the drift study uses.
+    w = oracle.storage(oracle.normal(d * n, 13, std=0.5).reshape(d, n), w_dtype)
+    x = oracle.normal(n, 14)
+    oracle.set_gemv_order(descending)
+    try:
+        got, want = oracle.gemv(w, w_dtype, x), oracle.gemv_scalar(w, w_dtype, x)
+    finally:
+        oracle.set_gemv_order(False)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the descending order is a different summation order of the same sums
+    if descending and n > 8:
+        ref = oracle.widen(w, w_dtype).astype(np.float64) @ x.astype(np.float64)
+        assert np.max(np.abs(got - ref)) <= 1e-6 * np.sqrt(n) * np.max(np.abs(ref)) + 1e-6
+
+
 def test_add_is_elementwise():
     # tests/kernels.rs:224-237
     np.testing.assert_array_equal(oracle.add(np.array([1.0, 2.0]), np.array([3.0, 4.0])), [4, 6])
@@ -411,6 +433,37 @@ def test_model_kv_cache_holds_rope_of_projection():
     np.testing.assert_allclose(v[0].reshape(-1), oracle.gemv(w["wv"][0], F32, xb.reshape(-1)),
                                rtol=0, atol=0)
     assert np.all(k[2:] == 0) and np.all(v[2:] == 0)
+
+
+@pytest.mark.parametrize("kv_dtype", [F32, BF16])
+def test_model_kv_hooks(kv_dtype):
+    # kv_rows() returns exactly what a step stores at its position; with
+    # stores off the cache is left as written; writing a step's own rows
+    # and stepping with stores off gives the stored step's logits bit for
+    # bit.
+    cfg = oracle.LlamaConfig(**TINY, kv_dtype=kv_dtype)
+    w = oracle.random_weights(cfg, seed=21, std=0.3)
+    ref, m = oracle.Model(cfg, dict(w)), oracle.Model(cfg, dict(w))
+    tokens = [5, 1, 9, 40, 3]
+    for pos, tok in enumerate(tokens):
+        want = ref.step(tok, pos)
+        for layer in range(cfg.n_layers):
+            k, v = ref.kv_layer(layer)
+            rk, rv = ref.kv_rows(layer)
+            np.testing.assert_array_equal(k[pos], rk)
+            np.testing.assert_array_equal(v[pos], rv)
+            m.write_kv(layer, pos, rk[None], rv[None])
+        m.set_kv_store(False)
+        got = m.step(tok, pos)
+        m.set_kv_store(True)
+        np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # with stores off a step leaves the cache untouched
+    k_before, _ = m.kv_layer(0)
+    m.set_kv_store(False)
+    m.step(7, len(tokens))
+    np.testing.assert_array_equal(m.kv_layer(0)[0], k_before)
+    with pytest.raises(ValueError):
+        m.write_kv(0, cfg.max_seq, k_before[:1], k_before[:1])
 
 
 def test_generate_tokens_semantics():
