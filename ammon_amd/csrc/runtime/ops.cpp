@@ -192,10 +192,9 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
     }
     if (w == 1 || w <= max_per_cu / 2) break;
   }
-  // QKV: at most two workgroups per CU, even with a ragged last round --
-  // every workgroup stages and normalises all of x before its first tile,
-  // and at the Llama-3-8B shape (768 row blocks) 512 workgroups measured
-  // 11.2 us against 12.1 for 768
+  // QKV: at most two workgroups per CU, even with a ragged last round: at
+  // the Llama-3-8B shape (768 row blocks) 512 workgroups measured 10.4-10.6
+  // us against 11.5-11.6 for 768 (x requested ahead of the weights)
   if (a.mode == AMMON_GEMV_QKV && max_per_cu > 2) grid = std::min<uint32_t>(p.row_blocks, cus * 2);
   if (a.mode == AMMON_GEMV_PLAIN_ARGMAX)
     AMMON_CHECK(grid <= a.cand_cap, "%s: scratch holds %u candidates, the launch needs %u", what,

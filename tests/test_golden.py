@@ -23,3 +23,30 @@ def test_c1_fixture_is_reproduced_by_the_oracle():
     assert len(tokens) == 255
     np.testing.assert_array_equal(tokens[:7], prompt[1:])
     assert np.all((prompt >= 1) & (prompt < 32000))
+
+
+def test_c4_bf16kv_drift_fixture_states_what_the_gpu_test_relies_on():
+    """The drift study (oracle against itself, one GEMV summation order
+    changed) with a bf16 cache drifts ~100x more than with an fp32 cache and
+    flips a greedy pick; with an fp32 cache it does not within the fixture's
+    527 steps."""
+    import make_bf16kv_drift
+    f = np.load(os.path.join(HERE, "golden", "c4_bf16kv_drift.npz"))
+    assert json.loads(str(f["config"])) == make_bf16kv_drift.C4
+    prompt = make_bf16kv_drift.prompt_tokens()
+    np.testing.assert_array_equal(prompt, f["prompt"])
+    for kv in ("bf16", "f32"):
+        ta, tb, first = f[f"{kv}_tokens_a"], f[f"{kv}_tokens_b"], int(f[f"{kv}_first_divergent"])
+        np.testing.assert_array_equal(ta[:15], prompt[1:])
+        agree = len(ta) if first < 0 else first
+        np.testing.assert_array_equal(ta[:agree], tb[:agree])
+        if first >= 0:
+            assert first == len(ta) - 1 and ta[first] != tb[first]
+            # the flipped pick is one of the few steps with a tiny top-2 margin
+            m = f[f"{kv}_margins_a"]
+            assert m[first] < np.percentile(m, 5)
+    assert int(f["bf16_first_divergent"]) == 358
+    assert int(f["f32_first_divergent"]) == -1 and len(f["f32_tokens_a"]) == 527
+    bf, fp = f["bf16_drift"], f["f32_drift"]
+    assert np.median(bf) > 30 * np.median(fp)
+    assert bf[0] > 1e-3 and fp.max() < 1e-4

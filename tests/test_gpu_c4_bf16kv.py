@@ -10,7 +10,9 @@ elements of a row to neighbouring bf16 values.  Those rows then feed every
 later step, so the two decodes drift apart until a greedy pick with a small
 top-2 margin flips.  tests/golden/c4_bf16kv_drift.npz measures this with the
 oracle against itself (one GEMV summation order changed): the logits differ
-by ~3e-3 normwise from the first step on.
+by 2e-3 to 3.7e-3 normwise from the first step on and the greedy picks part
+at step 358; with an fp32 cache the difference stays below 5.1e-5 and no pick
+flips in 527 steps.
 
 So the test keeps the two caches identical.  At each position the GPU steps
 first (the production launch list, its own K / V stores); its rows at that
@@ -21,11 +23,14 @@ summation order inside the one step: normwise relative error <= 1e-4 (the
 fp32-cache C4 run measures 2.9e-5 after 527 steps).  The greedy pick must be
 the oracle's, unless the oracle's top-2 margin is within 2 |logits error|_inf
 (the largest gap that error can close); the count of such steps is printed
-and must be 0 here.  Both sides are then fed the oracle's token.  Every 16
-steps the oracle also stores its own rows at a position first, and its rows
-are compared with the GPU's: each stored element equal or one bf16 ulp
-apart, <= 2^-7 normwise per row (the rounding of fp32 rows that differ by
-summation order).
+and must be 0 here.  Both sides are then fed the oracle's token.  At every
+position the rows the oracle computed (and did not store) are compared with
+the GPU's: every element within one bf16 ulp of its magnitude plus 1e-4 of
+its row's largest element.  The two fp32 rows before rounding differ by
+summation order, inside this layer's projection and in the hidden state the
+earlier layers of the same step built over the same cache (the same cause,
+and so the same normwise bar, as the logits); rounding each to bf16 then
+moves an element by at most one ulp.
 
 Two phases: the 16-token prompt drawn with seed 1004 (the first seed of
 the range the fp32 fixture chose from, taken without screening) and 64
@@ -50,8 +55,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 FIXTURE = os.path.join(HERE, "golden", "c4_greedy.npz")
 PROMPT_SEED = 1004
 LOGITS_TOL = 1e-4
-ROW_TOL = 2.0 ** -7
-CHECK_ROWS_EVERY = 16
+ROW_FP32_TOL = 1e-4
 
 
 class Cfg:
@@ -130,37 +134,45 @@ def gpu_rows(model, cfg, pos):
     return rows
 
 
+def bf16_ulp(v):
+    """Spacing of bf16 values at |v| (7 stored mantissa bits)."""
+    v = np.abs(np.asarray(v, np.float64))
+    e = np.floor(np.log2(np.where(v > 0, v, 1.0)))
+    return np.where(v > 0, np.exp2(e - 7), 2.0 ** -133)
+
+
 def check_rows(got_rows, orc, cfg):
-    """Each oracle-stored row vs the GPU's: normwise <= 2^-7, each element
-    equal or one bf16 ulp apart.  Returns the count of differing elements."""
-    flips = 0
+    """Each oracle-stored row (one kv head) vs the GPU's: every element must
+    satisfy |got - want| <= ulp(max(|got|, |want|)) + ROW_FP32_TOL max |want|
+    (fp32 rows apart by summation order, each rounded to bf16).  Returns (worst
+    normwise difference, worst fp32 part -- the excess over one ulp relative
+    to the row's largest element --, count of elements that differ)."""
+    worst, excess, differ = 0.0, 0.0, 0
     for layer, (gk, gv) in enumerate(got_rows):
         ok_, ov = orc.kv_rows(layer)
         for got, want in ((gk, ok_), (gv, ov)):
-            g32, w32 = oracle.widen(got, oracle.BF16), oracle.widen(want, oracle.BF16)
+            g32 = oracle.widen(got, oracle.BF16).astype(np.float64)
+            w32 = oracle.widen(want, oracle.BF16).astype(np.float64)
             for h in range(cfg.n_kv_heads):
-                assert rel_err(g32[h], w32[h]) <= ROW_TOL, (layer, h)
-            ulps = np.abs(got.astype(np.int32) - want.astype(np.int32))
-            assert int(ulps.max()) <= 1, (layer, int(ulps.max()))
-            flips += int(np.count_nonzero(ulps))
-    return flips
+                ulp = bf16_ulp(np.maximum(np.abs(g32[h]), np.abs(w32[h])))
+                peak = np.max(np.abs(w32[h]))
+                diff = np.abs(g32[h] - w32[h])
+                assert np.all(diff <= ulp + ROW_FP32_TOL * peak), (layer, h)
+                worst = max(worst, rel_err(g32[h], w32[h]))
+                excess = max(excess, float(np.max(np.maximum(diff - ulp, 0.0))) / peak)
+            differ += int(np.count_nonzero(got != want))
+    return worst, excess, differ
 
 
 def run_synced(gpu, orc, cfg, first_token, positions, forced=()):
     """Step both sides over `positions` with identical caches (see the module
     docstring); returns the per-step (logits error, oracle margin)."""
     token = first_token
-    worst, ties, flips, checked = 0.0, 0, 0, 0
+    worst, ties, flips, row_worst, row_excess = 0.0, 0, 0, 0.0, 0.0
     t0 = time.time()
     for i, pos in enumerate(positions):
         lg = gpu.step(token, pos)
         rows = gpu_rows(gpu, cfg, pos)
-        if i % CHECK_ROWS_EVERY == 0:
-            # the oracle's own rows at this position, then the GPU's in their place
-            orc.set_kv_store(True)
-            orc.step(token, pos)
-            flips += check_rows(rows, orc, cfg)
-            checked += 1
         for layer, (k, v) in enumerate(rows):
             orc.write_kv(layer, pos, k[None], v[None])
         orc.set_kv_store(False)
@@ -168,6 +180,9 @@ def run_synced(gpu, orc, cfg, first_token, positions, forced=()):
             lo = orc.step(token, pos)
         finally:
             orc.set_kv_store(True)
+        # the rows the oracle computed at this position over the same cache
+        e, x, d = check_rows(rows, orc, cfg)
+        row_worst, row_excess, flips = max(row_worst, e), max(row_excess, x), flips + d
         err = rel_err(lg, lo)
         worst = max(worst, err)
         assert err <= LOGITS_TOL, (pos, err)
@@ -181,9 +196,11 @@ def run_synced(gpu, orc, cfg, first_token, positions, forced=()):
         if i % 16 == 15:
             log(f"  pos {pos}: worst logits error so far {worst:.2e} "
                 f"({(i + 1) / (time.time() - t0):.2f} steps/s)")
+    n_elems = len(positions) * cfg.n_layers * 2 * cfg.dim // cfg.n_heads * cfg.n_kv_heads
     log(f"  {len(positions)} steps: logits error <= {worst:.2e} (bar {LOGITS_TOL:g}); picks inside "
-        f"the error bound: {ties}; rows checked at {checked} positions, {flips} elements one bf16 "
-        f"ulp apart")
+        f"the error bound: {ties}; K / V rows at every position: each element "
+        f"within one bf16 ulp + {row_excess:.2e} of the row's largest (bar {ROW_FP32_TOL:g}), "
+        f"normwise <= {row_worst:.2e}, {flips} of {n_elems} elements differ")
     return worst, ties
 
 
