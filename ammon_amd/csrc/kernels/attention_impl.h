@@ -424,18 +424,24 @@ struct AttnPartialMfmaStaged {
     return (u32x4 *)lds + ((b * 2 + kv) * 16 + w * 4 + i) * 64;
   }
 
-  // Request chunk c of the split into ring buffer b.  K: request kk brings
-  // row 16w + (l % 16) of the chunk, dims 32(l / 16) + 8kk..+7 (the score
-  // MFMA's A fragment of lane l).  V: request i brings row r = 4i + l / 16
-  // of the wave's 16, 16-byte piece (l % 16 + 2i) % 16 -- so the wave's V
-  // block is [row][slot], slot s of row r holding dims 8((s + 2(r / 4)) %
-  // 16)..+7.  Rows at or past the split's end read as zero.
+  // Request chunk c of the split into ring buffer b; every request of a
+  // wave brings four whole 256-byte rows (1 KiB contiguous: a request that
+  // gathered 16 rows x 16-byte pieces instead ran 1.1 us slower per 33.5 MB
+  // launch).  K: request kk brings row r = 4kk + l / 16 of the wave's 16,
+  // 16-byte piece (l % 16 + r) % 16 -- so the wave's K block is [row][slot],
+  // slot s of row r holding dims 8((s + r) % 16)..+7, and the 16 lanes that
+  // read one piece of 16 rows for the score MFMA hit 16 distinct slots.  V:
+  // request i brings row r = 4i + l / 16, piece (l % 16 + 2i) % 16 -- slot s
+  // of row r holding dims 8((s + 2(r / 4)) % 16)..+7.  Rows at or past the
+  // split's end read as zero.
   AMMON_DEV void stage(float *lds, uint32_t c, uint32_t b) const {
     const uint32_t c0 = c * CHUNK + 16 * wave;
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
-      const uint32_t tk = c0 + (lane & 15);
-      const uint32_t off = tk < n ? (tk * HEAD + 32 * (lane >> 4) + 8 * kk) * 2 : AMMON_OOB;
+      const uint32_t r = 4 * kk + (lane >> 4);
+      const uint32_t tk = c0 + r;
+      const uint32_t piece = ((lane & 15) + r) & 15;
+      const uint32_t off = tk < n ? (tk * HEAD + 8 * piece) * 2 : AMMON_OOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           kres, (__attribute__((address_space(3))) void *)slot_base(lds, b, 0, wave, kk), 16,
           off, 0, 0, 0);
@@ -516,6 +522,13 @@ struct AttnPartialMfmaStaged {
       qlo[kk] = __builtin_convertvector(f - __builtin_convertvector(qhi[kk], f32x8), bf16x8);
     }
 
+    // The score MFMA's A fragment kk of lane l: row l % 16 of the wave's K
+    // block, dims 32(l / 16) + 8kk..+7 (q's B fragment kk holds the same
+    // dims): piece 4(l / 16) + kk, at slot (piece - row) % 16 of that row.
+    uint32_t kslot[4];
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) kslot[kk] = 16 * h + ((4 * grp + kk - h) & 15);
+
     // O^T tiles: lane l holds dims 16nt + 4(l / 16) + r of head l % 16
     f32x4 o[8];
 #pragma unroll
@@ -550,7 +563,7 @@ struct AttnPartialMfmaStaged {
         f32x4 sh = {0.f, 0.f, 0.f, 0.f}, sl = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kk = 0; kk < 4; ++kk) {
-          const bf16x8 a = __builtin_bit_cast(bf16x8, slot_base(lds, c % NCH, 0, wave, kk)[lane]);
+          const bf16x8 a = __builtin_bit_cast(bf16x8, slot_base(lds, c % NCH, 0, wave, 0)[kslot[kk]]);
           sh = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qhi[kk], sh, 0, 0, 0);
           sl = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, qlo[kk], sl, 0, 0, 0);
         }
