@@ -72,6 +72,7 @@ SIGNATURES = {
     "ammon_fill": (_ST, [_P, _P, _P, _DT, _SZ, _F]),
     "ammon_fill_normal": (_ST, [_P, _P, _P, _DT, _SZ, _U64, _U64, _F, _F]),
     "ammon_checksum": (_ST, [_P, _P, _P, _SZ, _P]),
+    "ammon_stream_read": (_ST, [_P, _P, _P, _SZ]),
     "ammon_rope_table_bytes": (_SZ, [_U32, _U32]),
     "ammon_rope_table_host": (_ST, [_F, _U32, _U32, _P]),
     "ammon_kv_unpermute": (_ST, [_P, _P, _U32, _U32, _U32, _U32]),

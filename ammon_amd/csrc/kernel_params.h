@@ -155,6 +155,12 @@ typedef struct {
 } ammon_k_checksum;
 
 typedef struct {
+  const void *src;          /* 16-byte aligned */
+  uint64_t bytes;
+  uint64_t share;           /* bytes per workgroup: a multiple of 16 KiB, < 2^32 */
+} ammon_k_stream_read;
+
+typedef struct {
   void *dst;
   uint64_t count, seed, stream;
   float mean, std;

@@ -120,6 +120,46 @@ extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_checksum(ammon_k_ch
   }
 }
 
+// ---- streaming read ------------------------------------------------------------
+// Reads src[0, bytes) once and keeps nothing: the floor for a launch that
+// moves that many bytes.  Workgroup w reads bytes [w share, (w + 1) share)
+// in windows of 16 KiB (four 16-byte loads per lane, 1 KiB contiguous per
+// wave and load), requesting the next window before folding the current one;
+// the loads go through a buffer resource bounded to the share, so a tail
+// past the buffer reads zero without touching memory.  The folded value is
+// consumed by an empty asm statement: no store, no atomic.
+#define SR_WIN 4
+extern "C" __global__ __launch_bounds__(AMMON_WG) void ammon_stream_read(ammon_k_stream_read p) {
+  constexpr uint32_t win_bytes = AMMON_WG * SR_WIN * 16;
+  const uint64_t start = (uint64_t)blockIdx.x * p.share;
+  const uint32_t len =
+      start >= p.bytes ? 0u : (uint32_t)(p.bytes - start < p.share ? p.bytes - start : p.share);
+  const __amdgpu_buffer_rsrc_t r =
+      make_rsrc((const char *)p.src + (start >= p.bytes ? 0 : start), len);
+  const uint32_t rounds = (uint32_t)(p.share / win_bytes);
+  uint32_t off = threadIdx.x * 16u;
+  u32x4 a[SR_WIN], b[SR_WIN];
+  u32x4 x = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int u = 0; u < SR_WIN; ++u)
+    a[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off + u * AMMON_WG * 16u, 0, AMMON_WEIGHT_CPOL);
+  for (uint32_t k = 1; k < rounds; ++k) {
+    off += win_bytes;
+#pragma unroll
+    for (int u = 0; u < SR_WIN; ++u)
+      b[u] = __builtin_amdgcn_raw_buffer_load_b128(r, off + u * AMMON_WG * 16u, 0, AMMON_WEIGHT_CPOL);
+#pragma unroll
+    for (int u = 0; u < SR_WIN; ++u) {
+      x ^= a[u];
+      a[u] = b[u];
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < SR_WIN; ++u) x ^= a[u];
+  const uint32_t f = x[0] ^ x[1] ^ x[2] ^ x[3];
+  asm volatile("" ::"v"(f));
+}
+
 // ---- fills -----------------------------------------------------------------
 AMMON_DEV uint64_t splitmix64(uint64_t x) {
   x += 0x9E3779B97F4A7C15ull;

@@ -45,6 +45,7 @@ struct Kernels {
   hipFunction_t fill_normal = nullptr;
   hipFunction_t fill_const = nullptr;
   hipFunction_t checksum = nullptr;
+  hipFunction_t stream_read = nullptr;
   // prefill GEMMs on matrix cores: [weight dtype][16 / 32-token tiles]
   // [row tile per wave / split over the workgroup's waves][mode]
   hipFunction_t gemm[2][2][2][kGemvModes] = {};

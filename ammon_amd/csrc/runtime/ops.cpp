@@ -1124,4 +1124,25 @@ ammon_status ammon_checksum(ammon_runtime *rt, ammon_stream stream, const void *
   return launch(rt, stream, rt->k.checksum, grid, 1, 0, p, "checksum");
 }
 
+ammon_status ammon_stream_read(ammon_runtime *rt, ammon_stream stream, const void *src,
+                               size_t bytes) {
+  REQUIRE_RT();
+  AMMON_CHECK(bytes == 0 || src != nullptr, "stream_read: NULL src");
+  AMMON_CHECK(((uintptr_t)src & 15) == 0, "stream_read: src must be 16-byte aligned");
+  VALIDATE_ONLY();
+  if (bytes == 0) return AMMON_OK;
+  // two workgroups per CU, each a contiguous share in 16 KiB windows: the
+  // fastest read of 32 MiB - 3.5 GiB in a chained sweep of layouts (one share
+  // or a device-wide sweep per window; 1, 2 or 4 workgroups per CU; 4 or 8
+  // loads in flight per lane)
+  const uint64_t win = (uint64_t)kWorkgroup * 4 * 16;
+  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
+  const uint32_t grid = (uint32_t)std::min<uint64_t>(2ull * cus, cdiv((uint64_t)bytes, win));
+  const uint64_t share = cdiv(cdiv((uint64_t)bytes, (uint64_t)grid), win) * win;
+  AMMON_CHECK(share <= (1ull << 31), "stream_read: %zu bytes exceed %llu per workgroup", bytes,
+              (unsigned long long)(1ull << 31));
+  ammon_k_stream_read p = {src, (uint64_t)bytes, share};
+  return launch(rt, stream, rt->k.stream_read, grid, 1, 0, p, "stream_read");
+}
+
 }  // extern "C"

@@ -145,6 +145,7 @@ static ammon_status load_kernels(ammon_runtime *rt) {
   R(5, "ammon_fill_normal", k.fill_normal);
   R(5, "ammon_fill_const", k.fill_const);
   R(5, "ammon_checksum", k.checksum);
+  R(5, "ammon_stream_read", k.stream_read);
   for (int d = 0; d < 2; ++d)
     for (int t = 0; t < 2; ++t)
       for (int s = 0; s < 2; ++s)

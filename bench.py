@@ -389,39 +389,65 @@ def rate(nbytes, us):
             "frac": round(gbs / HBM_PEAK_GBS, 4)}
 
 
-def stream_ceiling(rt, model):
-    """The device's plain streaming-read rate: ammon_checksum (one workgroup
-    per CU sweeping the buffer with nontemporal 16-byte loads, two integer
-    ops per 8 bytes) over slices of the 3.76 GB gate matrix stack.  Per
-    size, a captured graph of back-to-back launches over distinct slices
-    (so no launch finds its bytes in a cache), median of 5 replays: the
-    time a pure read of that many bytes takes as one launch, fixed costs
-    included -- the floor for a kernel of that size."""
-    from ammon_amd._abi import F32, call
-    buf = model.weights["w1"]
-    out = rt.alloc(16)
-    stream = model.stream
-    sizes = {}
-    for nbytes in (33554432, 234881024, 1073741824, buf.nbytes):
-        n = min(buf.nbytes // nbytes, 16)
+def read_chain_us(rt, stream, sources, nbytes, max_launches=32):
+    """Per-launch µs of a captured graph of back-to-back ammon_stream_read
+    launches of `nbytes` each over distinct slices of the `sources` buffers
+    (so no launch finds its bytes in a cache), median of 5 replays."""
+    from ammon_amd._abi import call
+    nbytes = -(-int(nbytes) // 16) * 16
+    slices = [int(b) + i * nbytes for b in sources for i in range(b.nbytes // nbytes)]
+    slices = slices[:max_launches]
 
-        def launch_all(nbytes=nbytes, n=n):
-            for i in range(n):
-                call("ammon_checksum", rt.handle, stream, ctypes.c_void_p(int(buf) + i * nbytes),
-                     nbytes, out)
-        # each checksum call first zeroes its two result words with a
-        # one-workgroup fill launch: timed alone and subtracted
-        def fills(n=n):
-            for _ in range(n):
-                call("ammon_fill", rt.handle, stream, out, F32, 4, 0.0)
-        ms = (graph_ms(rt, stream, launch_all) - graph_ms(rt, stream, fills)) / n
-        sizes[str(nbytes)] = rate(nbytes, ms * 1e3)
-        log(f"stream read {nbytes / 2**20:7.0f} MiB: {ms * 1e3:8.2f} us "
-            f"({sizes[str(nbytes)]['gbs']:.0f} GB/s)")
-    r = dict(sizes[str(buf.nbytes)])
-    r["kernel"] = "ammon_checksum (plain streaming read, one workgroup per CU)"
-    r["by_size"] = sizes
-    return r
+    def launch_all():
+        for ptr in slices:
+            call("ammon_stream_read", rt.handle, stream, ctypes.c_void_p(ptr), nbytes)
+    return graph_ms(rt, stream, launch_all) * 1e3 / len(slices)
+
+
+# launches per token of each timed kernel in the decode graph; embed and the
+# argmax's second pass (kilobytes each) are the two others
+LAUNCHES = {"qkv_rope_store": 32, "attention_partial": 32, "attention_combine": 32,
+            "wo_residual": 32, "gate_up_swiglu": 32, "w2_residual": 32, "lm_head": 1}
+
+
+def launch_floor(rt, model, kernels, ms_per_step):
+    """The read floor of the decode's launch list.  For each launch, the
+    chained time of a pure read of its algorithmic bytes (ammon_stream_read:
+    two workgroups per CU, contiguous shares, nothing written), against the
+    kernel's own average; 32 x the per-layer launches + the LM head + two
+    kilobyte launches (embed, the argmax's second pass, each floored by a
+    16 KiB read) give the token time of a launch list whose every kernel
+    streamed like a plain read.  Sources: the w1, w2 and w3 stacks (3.76 GB
+    each).  Also the plain read of a whole stack (the device's streaming
+    ceiling)."""
+    srcs = [model.weights[n] for n in ("w1", "w2", "w3")]
+    stream = model.stream
+    by = {}
+    floor_ms = 2 * read_chain_us(rt, stream, srcs, 16384) * 1e-3
+    for name, n in LAUNCHES.items():
+        k = kernels[name]
+        f = read_chain_us(rt, stream, srcs, k["bytes"])
+        by[name] = {"bytes": k["bytes"], "floor_us": round(f, 3), "kernel_us": k["avg_us"],
+                    "excess_us": round(k["avg_us"] - f, 3), "launches_per_token": n}
+        floor_ms += n * f * 1e-3
+        log(f"read floor {name:18s} {k['bytes'] / 1e6:9.1f} MB: {f:8.2f} us "
+            f"(kernel {k['avg_us']:.2f} us, +{k['avg_us'] - f:.2f})")
+    log(f"launch-list read floor {floor_ms:.4f} ms/token = {1e3 / floor_ms:.1f} tok/s; "
+        f"measured {ms_per_step:.4f} ms ({floor_ms / ms_per_step:.3f} of the floor's rate)")
+    floor = {"kernel": "ammon_stream_read (pure read, 2 workgroups per CU, contiguous shares)",
+             "by_launch": by, "ms_per_token": round(floor_ms, 4),
+             "tokens_per_s": round(1e3 / floor_ms, 1),
+             "measured_ms_per_token": round(ms_per_step, 4),
+             "measured_over_floor_rate": round(floor_ms / ms_per_step, 4)}
+    sizes = {}
+    for nbytes in (1073741824, srcs[0].nbytes):
+        us = read_chain_us(rt, stream, srcs, nbytes)
+        sizes[str(nbytes)] = rate(nbytes, us)
+        log(f"stream read {nbytes / 2**20:7.0f} MiB: {us:8.2f} us ({sizes[str(nbytes)]['gbs']:.0f} GB/s)")
+    ceiling = dict(sizes[str(srcs[0].nbytes)])
+    ceiling["kernel"] = "ammon_stream_read (pure read, 2 workgroups per CU, contiguous shares)"
+    ceiling["by_size"] = sizes
+    return floor, ceiling
 
 
 C3_CTX = (1024, 4096, 8192)
@@ -916,7 +942,7 @@ def main():
     if not args.no_configs:
         cb = 0.0 if args.no_cpu else args.cpu_budget
         small = 0.5 if cb > 0 else 0.0
-        for name, fn in (("stream_read_ceiling", lambda: stream_ceiling(rt, model)),
+        for name, fn in (("launch_floor", lambda: launch_floor(rt, model, kernels, ms_per_step)),
                          ("c3", lambda: c3_attention(rt, stream, small)),
                          ("c2", lambda: c2_kernels(rt, stream, model.weights["tok_emb"], small)),
                          ("c1", lambda: c1_decode(rt, cb)),
@@ -928,6 +954,9 @@ def main():
                 extras[name] = {"error": f"{type(e).__name__}: {e}"}
                 log(f"{name} failed: {extras[name]['error']}")
 
+    # (floor, ceiling), or an error record in the floor's place
+    lf = extras.pop("launch_floor", None)
+    floor, ceiling = lf if isinstance(lf, tuple) else (lf, None)
     result = {
         "metric": METRIC,
         "value": round(tps, 3),
@@ -970,7 +999,8 @@ def main():
         "kernels": kernels,
         "prefill": prefill,
         "cpu_baseline": cpu,
-        "stream_read_ceiling": extras.get("stream_read_ceiling"),
+        "launch_floor": floor,
+        "stream_read_ceiling": ceiling,
         "configs": {k: extras[k] for k in ("c1", "c2", "c3", "c4", "c5") if k in extras},
     }
     model.close()

@@ -144,10 +144,15 @@ ammon_status ammon_fill_normal(ammon_runtime *rt, ammon_stream stream, void *dst
  * and out[1] = xor of the little-endian 64-bit words of src[0, bytes) (bytes
  * a multiple of 8, src 16-byte aligned; out is 2 words of device memory).
  * Proves two copies of a tensor identical bit for bit (device-generated
- * weights against a host fixture) without moving them; as a plain streaming
- * read it also gives the device's HBM read ceiling. */
+ * weights against a host fixture) without moving them. */
 ammon_status ammon_checksum(ammon_runtime *rt, ammon_stream stream, const void *src, size_t bytes,
                             uint64_t *out);
+/* Streaming read (no counterpart in the reference): reads src[0, bytes) once
+ * (src 16-byte aligned) and writes nothing.  A chain of these over distinct
+ * buffers measures the floor of a launch that moves that many bytes -- the
+ * benchmark's per-size read floor. */
+ammon_status ammon_stream_read(ammon_runtime *rt, ammon_stream stream, const void *src,
+                               size_t bytes);
 
 /* ---- host utilities (no device needed) ----------------------------------- */
 

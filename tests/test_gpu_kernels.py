@@ -705,6 +705,20 @@ def test_checksum_matches_numpy(rt, nbytes):
         call("ammon_checksum", rt.handle, None, buf, 12, out)
 
 
+def test_stream_read_runs_at_every_size_and_leaves_memory_alone(rt):
+    # a pure read: sizes below one window, ragged tails and several windows
+    # per workgroup complete (the buffer resource reads past-the-end bytes as
+    # zero) and the buffer is unchanged; misaligned sources are refused
+    words = np.arange(1 << 21, dtype=np.uint64)
+    buf = up(rt, words)
+    for nbytes in (0, 16, 40, 16384 + 16, 3 << 20, words.nbytes):
+        call("ammon_stream_read", rt.handle, None, buf, nbytes)
+    rt.synchronize()
+    np.testing.assert_array_equal(down(buf, words.size, np.uint64), words)
+    with pytest.raises(AmmonError, match="16-byte aligned"):
+        call("ammon_stream_read", rt.handle, None, ctypes.c_void_p(int(buf) + 8), 64)
+
+
 def test_fill_const(rt):
     buf = rt.alloc(1000 * 4)
     rt.fill(buf, F32, 1000, 2.5)
