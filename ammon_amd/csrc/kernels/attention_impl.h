@@ -352,9 +352,9 @@ AMMON_DEV void wave_lds_order() {
 // acc = sum_w acc_w 2^(m_w - M), l = sum_w l_w 2^(m_w - M).  The partial
 // format is the other units': (sum_t e^{s_t - m} V_t, m, l).
 //
-// V rows are staged with their 16-byte pieces rotated by 2(row / 4) slots
-// (row = the wave's position 0..15), so the 16-bit column reads of the four
-// lane groups (rows 4g + i) fall in distinct LDS banks.
+// V rows are staged with their 16-byte pieces rotated (by 2 (row % 4) +
+// 8 ((row / 4) % 2) slots, row = the wave's position 0..15) so that the
+// transposing reads of the P.V operand fall in distinct LDS banks.
 //
 // LDS: att_staged_lds_floats(GMAX, NCH) floats (the merge's rows reuse the
 // chunk buffers).
@@ -431,9 +431,12 @@ struct AttnPartialMfmaStaged {
   // 16-byte piece (l % 16 + r) % 16 -- so the wave's K block is [row][slot],
   // slot s of row r holding dims 8((s + r) % 16)..+7, and the 16 lanes that
   // read one piece of 16 rows for the score MFMA hit 16 distinct slots.  V:
-  // request i brings row r = 4i + l / 16, piece (l % 16 + 2i) % 16 -- slot s
-  // of row r holding dims 8((s + 2(r / 4)) % 16)..+7.  Rows at or past the
-  // split's end read as zero.
+  // request i brings row r = 4i + l / 16, piece (l % 16 + rv(r)) % 16 with
+  // rv(r) = 2 (r % 4) + 8 ((r / 4) % 2) -- slot s of row r holding dims
+  // 8((s + rv(r)) % 16)..+7, so the transposing reads of v_frag (four rows'
+  // 32-byte runs per 16 lanes, two lane groups per half-wave) fall on eight
+  // distinct 32-byte bank ranges.  Rows at or past the split's end read as
+  // zero.
   AMMON_DEV void stage(float *lds, uint32_t c, uint32_t b) const {
     const uint32_t c0 = c * CHUNK + 16 * wave;
 #pragma unroll
@@ -449,7 +452,7 @@ struct AttnPartialMfmaStaged {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const uint32_t tv = c0 + 4 * i + (lane >> 4);
-      const uint32_t piece = ((lane & 15) + 2 * i) & 15;
+      const uint32_t piece = ((lane & 15) + 2 * (lane >> 4) + 8 * (i & 1)) & 15;
       const uint32_t off = tv < n ? (tv * HEAD + 8 * piece) * 2 : AMMON_OOB;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(
           vres, (__attribute__((address_space(3))) void *)slot_base(lds, b, 1, wave, i), 16,
@@ -493,16 +496,17 @@ struct AttnPartialMfmaStaged {
   }
 
   // The V^T A fragment of dims 16nt..16nt+15 from the wave's staged V block:
-  // lane l gets V[4(l / 16) + i][16nt + l % 16], i = 0..3.
+  // lane l gets V[4(l / 16) + i][16nt + l % 16], i = 0..3, by one transposing
+  // LDS read (ds_read_b64_tr_b16: within each 16-lane group, lane m receives
+  // element m % 4 of the 8-byte blocks addressed by lanes m / 4 + 4i).  So
+  // lane s of group g addresses row 4g + s / 4, dims 16nt + 4(s % 4)..+3.
   AMMON_DEV static i16x4 v_frag(const float *vblk, uint32_t lane, int nt) {
-    const uint16_t *v = (const uint16_t *)vblk;
-    const uint32_t grp = lane >> 4, d = 16 * nt + (lane & 15);
-    // row 4 grp + i sits at rotation 2 grp: slot (d / 8 - 2 grp) % 16
-    const uint32_t col = ((((d >> 3) - 2 * grp) & 15) << 3) | (d & 7);
-    i16x4 f;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) f[i] = (short)v[(4 * grp + i) * HEAD + col];
-    return f;
+    const uint32_t s = lane & 15, g = lane >> 4, j = s >> 2, q = s & 3;
+    const uint32_t r = 4 * g + j;
+    const uint32_t slot = (2 * nt + (q >> 1) - (2 * j + 8 * (g & 1))) & 15;
+    const uint16_t *a = (const uint16_t *)vblk + r * HEAD + slot * 8 + (q & 1) * 4;
+    return __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4 *)(a));
   }
 
   AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
