@@ -4,15 +4,15 @@
 //
 // Pass 1, one workgroup per (split s, kv head g): positions
 // [s*S, s*S + S) clipped to t <= pos, for all G = q_heads / kv_heads query
-// heads of that kv head.  Each K and V byte is loaded once from HBM into
-// registers and used for all G heads (the reference re-reads it per q head).
-// A lane owns CH consecutive dims of one position (16-byte loads for bf16
-// head 128), so a wave covers 64 / P2 positions per pass over the head-major
-// cache [kv_heads, seq, head].  Each group of lanes keeps an online softmax
-// over the positions it sees; the groups are merged once at the end (LDS).
-// Writes partial[h, s, :] = (sum_t e^{score_t - m} V_t, m, l) with
-// the reference's layout [q_heads, splits, head + 2].  Splits that start past
-// pos write nothing.
+// heads of that kv head.  Each K and V byte is loaded once from HBM and used
+// for all G heads (the reference re-reads it per q head).  Two units run it:
+// AttnPartial (VALU, K/V in registers; fp32 caches and heads other than
+// 128), where a lane owns CH consecutive dims of one position and each group
+// of lanes keeps an online softmax over the positions it sees, merged once
+// at the end; and AttnPartialMfmaStaged (matrix cores, K/V staged in LDS;
+// bf16 caches of head 128), below.  Both write partial[h, s, :] =
+// (sum_t e^{score_t - m} V_t, m, l) with the reference's layout [q_heads,
+// splits, head + 2]; splits that start past pos write nothing.
 //
 // Pass 2, one workgroup per (q head, 8- or 32-dim slice): M = max m_s over live splits,
 // out = sum_s acc_s e^{m_s - M} / sum_s l_s e^{m_s - M}.
@@ -337,12 +337,12 @@ AMMON_DEV void wave_lds_order() {
 //
 // Arithmetic.  Wave w owns positions [16w, 16w + 16) of every chunk.
 //   scores  S^T[t][h] = sum_d K[t][d] q[h][d] on v_mfma_f32_16x16x32_bf16
-//           (A = K rows as stored, B = q^T with q split into bf16 hi + lo:
+//           (A = K rows from LDS, B = q^T with q split into bf16 hi + lo:
 //           ~16 bits of q, fp32 accumulation); heads >= G are padding;
 //   softmax per wave and head, in base 2: running max m and sum l; the
 //           weights P = 2^(s - m) are exact fp32 values;
 //   values  O^T[d][h] += sum_t V[t][d] P[h][t] on v_mfma_f32_16x16x16_bf16
-//           (A = V^T read from LDS, B = P^T straight from the score tile's
+//           (A = V^T by transposing LDS reads, B = P^T straight from the score tile's
 //           registers -- the score layout of a 16x16 tile is the 16x16x16
 //           B-operand layout), with P split into three bf16 parts
 //           (hi + mid + lo = P exactly), so every product is exact and only
@@ -352,9 +352,11 @@ AMMON_DEV void wave_lds_order() {
 // acc = sum_w acc_w 2^(m_w - M), l = sum_w l_w 2^(m_w - M).  The partial
 // format is the other units': (sum_t e^{s_t - m} V_t, m, l).
 //
-// V rows are staged with their 16-byte pieces rotated (by 2 (row % 4) +
-// 8 ((row / 4) % 2) slots, row = the wave's position 0..15) so that the
-// transposing reads of the P.V operand fall in distinct LDS banks.
+// Rows land in LDS with their 16-byte pieces rotated so the operand reads
+// are free of bank conflicts: K rows by the row index (the score operand
+// reads one piece of 16 rows per lane group), V rows by 2 (row % 4) +
+// 8 ((row / 4) % 2) slots (the transposing reads of the P.V operand take
+// four rows' 32-byte runs per 16 lanes); row = the wave's position 0..15.
 //
 // LDS: att_staged_lds_floats(GMAX, NCH) floats (the merge's rows reuse the
 // chunk buffers).
