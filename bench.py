@@ -668,8 +668,10 @@ def c4_generate(rt, cpu_budget):
     reference's formula (src/generate.rs:73-84: steps after the first over
     the time from the end of the first) for the device loop and the host
     loop.  With the reference's fp32 cache the tokens are checked against
-    the oracle's run stored in tests/golden/c4_greedy.npz (all 527); with a
-    bf16 cache (the headline's storage) the same loops are timed.  CPU leg:
+    the oracle's run stored in tests/golden/c4_greedy.npz: all 527 equal, or
+    equal up to a step where the runs part at a near tie (the oracle's top-2
+    margin within twice the logits' 1e-4 normwise tolerance); with a bf16
+    cache (the headline's storage) the same loops are timed.  CPU leg:
     the oracle on the same weights from the same prompt for a bounded number
     of steps, with token parity against the GPU's."""
     import oracle
@@ -681,6 +683,15 @@ def c4_generate(rt, cpu_budget):
     prompt = np.asarray(f["prompt"], np.int32)
     max_new = int(f["max_new_tokens"])
     want = np.asarray(f["tokens"], np.int32)
+    margins, scales = f["margins"].astype(np.float64), f["scales"].astype(np.float64)
+
+    def parity(got):
+        """True if equal, or equal up to a parting at a near tie."""
+        bad = np.nonzero(np.asarray(got) != want)[0]
+        if bad.size == 0:
+            return True
+        i = int(bad[0])
+        return i >= len(prompt) - 1 and margins[i] <= 2e-4 * scales[i]
     line = {"workload": "Llama-3-8B-shaped greedy decode, 16-token seeded prompt, "
                         f"max_new_tokens {max_new} ({max_new - 1} steps, "
                         f"{max_new - len(prompt)} generated); bf16 weights",
@@ -701,6 +712,7 @@ def c4_generate(rt, cpu_budget):
         if kv == F32:
             r["tokens_equal_oracle_fixture"] = bool(np.array_equal(toks, want) and
                                                    np.array_equal(toks_h, want))
+            r["tokens_match_oracle_up_to_near_tie"] = bool(parity(toks) and parity(toks_h))
             gpu_toks = toks
         line[kv_name] = r
         m.close()

@@ -6,8 +6,8 @@ reference's fp32 cache, measured with the oracle against itself.
 The model is the C4 fixture's (32 layers, dim 4096, 32 q / 8 kv heads of
 128, SwiGLU hidden 14336, vocab 128256, RoPE theta 500000, bf16 weights N(0,
 0.02) from weight seed 1003, RMSNorm weights 1, cache sized 8192).  The
-16-token prompt is drawn with seed 1004 -- the first seed of the range the
-fp32 fixture chose its prompt from, taken as is, with no screening.
+16-token prompt is drawn with seed 1004 -- the C4 fixture's prompt, taken
+by rule (the first seed of its range), with no screening.
 
 Run A is the oracle as it restates the reference (every GEMV row summed
 with j ascending, src/kernels.rs:54-73).  Run B is the same oracle with one

@@ -5,14 +5,14 @@ generator, RMSNorm weights 1, KV cache sized 8192) run through the oracle
 from a seeded 16-token prompt with max_new_tokens 528: 527 steps, 15 forced
 prompt tokens then 512 greedy picks (reference src/generate.rs:43-91).
 
-The KV cache is fp32, as in the reference (src/modules.rs:53-54): greedy
-tokens are compared bit for bit in fp32.  With a bf16 cache, two correct
-implementations whose fp32 K/V differ only by summation order store some
-elements one bf16 ulp apart (2^-8 relative), and 32 random-init layers
-amplify those flips over hundreds of steps until a top-2 margin of 4e-3
-flipped (measured).  The prompt seed is the one of 1004..1027 whose run has
-the widest smallest top-2 margin over the 512 generated steps (2.5e-3 on the
-GPU path), so the comparison is not decided by a near tie.
+The KV cache is fp32, as in the reference (src/modules.rs:53-54).  (With a
+bf16 cache a free-running comparison of two correct implementations parts
+after a few hundred steps: tests/golden/c4_bf16kv_drift.npz.)  The prompt
+is drawn with seed 1004, taken by rule (the first seed of the range the
+earlier fixtures drew from), not chosen for its margins; the test stops its
+token comparison at the first step whose top-2 margin the logits'
+tolerance could close, so that margins are stored per step with the
+step's logit scale.
 
 Stored:
   inputs   config, weight seed, prompt, max_new_tokens, and per weight tensor
@@ -21,7 +21,8 @@ Stored:
            weights elsewhere can prove they are the oracle's, bit for bit;
   outputs  the 527 chosen tokens, the last step's logits [128256], and for
            every step the gap between the largest and the second-largest
-           logit (top-2 margin) and the runner-up's index, so a mismatch can
+           logit (top-2 margin), the runner-up's index and the largest
+           |logit| (the scale of the normwise tolerance), so a mismatch can
            be told apart from a near tie.
 
 The oracle (C, OpenMP over output rows, each row in its serial order) is
@@ -44,7 +45,7 @@ import oracle  # noqa: E402
 C4 = dict(dim=4096, n_layers=32, n_heads=32, n_kv_heads=8, hidden=14336, vocab=128256,
           max_seq=8192, theta=500000.0, eps=1e-5)
 WEIGHT_SEED = 1003
-PROMPT_SEED = 1021
+PROMPT_SEED = 1004
 PROMPT_LEN = 16
 MAX_NEW_TOKENS = 528
 PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "c4_greedy.npz")
@@ -88,7 +89,7 @@ def run():
     prompt = c4_prompt()
     m = oracle.Model(cfg, weights)
     limit = min(MAX_NEW_TOKENS, cfg.max_seq)
-    tokens, margins, runners = [], [], []
+    tokens, margins, runners, scales = [], [], [], []
     token = int(prompt[0])
     logits = None
     t1 = time.time()
@@ -99,19 +100,21 @@ def run():
         tokens.append(nxt)
         margins.append(margin)
         runners.append(runner)
+        scales.append(float(np.max(np.abs(logits))))
         token = nxt
         if pos % 16 == 0:
             rate = (pos + 1) / (time.time() - t1)
             log(f"pos {pos}: next {nxt}, top-2 margin {margin:.3e}, {rate:.2f} steps/s")
     m.close()
     return prompt, np.array(tokens, np.int32), logits, np.array(margins, np.float32), \
-        np.array(runners, np.int32), sums
+        np.array(runners, np.int32), np.array(scales, np.float32), sums
 
 
 if __name__ == "__main__":
-    prompt, tokens, logits, margins, runners, sums = run()
+    prompt, tokens, logits, margins, runners, scales, sums = run()
     np.savez_compressed(PATH, prompt=prompt, tokens=tokens, logits=logits, margins=margins,
-                        runners=runners, config=json.dumps(C4), weight_seed=WEIGHT_SEED,
+                        runners=runners, scales=scales, config=json.dumps(C4),
+                        weight_seed=WEIGHT_SEED,
                         w_dtype=oracle.BF16, kv_dtype=oracle.F32,
                         max_new_tokens=MAX_NEW_TOKENS,
                         checksums=json.dumps({k: [str(s), str(x)] for k, (s, x) in sums.items()}))

@@ -50,3 +50,18 @@ def test_c4_bf16kv_drift_fixture_states_what_the_gpu_test_relies_on():
     bf, fp = f["bf16_drift"], f["f32_drift"]
     assert np.median(bf) > 30 * np.median(fp)
     assert bf[0] > 1e-3 and fp.max() < 1e-4
+
+
+def test_c4_fixture_is_the_drift_study_fp32_run():
+    """The C4 fixture (oracle, fp32 cache, seed-1004 prompt) and the drift
+    study's run A with the fp32 cache are the same decode, written by two
+    scripts: same prompt, same 527 tokens, same top-2 margins."""
+    f = np.load(os.path.join(HERE, "golden", "c4_greedy.npz"))
+    g = np.load(os.path.join(HERE, "golden", "c4_bf16kv_drift.npz"))
+    assert json.loads(str(f["config"])) == json.loads(str(g["config"]))
+    assert int(f["weight_seed"]) == int(g["weight_seed"])
+    np.testing.assert_array_equal(f["prompt"], g["prompt"])
+    np.testing.assert_array_equal(f["tokens"], g["f32_tokens_a"])
+    np.testing.assert_array_equal(f["margins"], g["f32_margins_a"])
+    # the largest |logit| per step is the scale of the 1e-4 normwise bar
+    assert f["scales"].shape == f["margins"].shape and np.all(f["scales"] > 0)

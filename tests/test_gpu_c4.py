@@ -8,15 +8,22 @@ src/generate.rs:43-91).
 
 The expected tokens come from tests/golden/c4_greedy.npz, written once by
 tests/golden/make_c4_fixture.py through the oracle on host-generated
-weights.  Here the same weights are generated on the device by the same
+weights, from a prompt drawn with the first seed of its range (no
+screening).  Here the same weights are generated on the device by the same
 seeded generator; every tensor's storage checksums must equal the fixture's
 before any token is compared, so the comparison is between identical
-models.  The greedy tokens must be identical; on a mismatch the message
-names the first differing step and the oracle's top-2 logit margin there,
-so a near tie can be told apart from a bug.  The last step's logits: the
-two sides differ only in fp32 summation order (~4e-6 relative per
-projection), compounded over 32 layers and 527 steps of cache: within 1e-4
-normwise relative.  The same holds for the device and the host loop.
+models.  The two sides' logits differ only in fp32 summation order (~4e-6
+relative per projection), compounded over 32 layers and the steps of cache:
+within DEEP_FP32_TOL = 1e-4 normwise relative, i.e. at most 1e-4 x the
+step's largest |logit| per element.  A greedy pick is therefore decided by
+arithmetic only where the oracle's top-2 margin exceeds twice that.  Every
+step is compared: the tokens must be identical, except that the runs may
+part at a generated step whose oracle margin is within that bound (a near
+tie; the comparison ends there and says so).  The closest step of this
+prompt is step 162: margin 1.03e-3 against a bound of 1.22e-3.  A mismatch
+anywhere else fails, naming the step and the oracle's margin there.  When
+no near tie parted the runs, the last step's logits must be within
+DEEP_FP32_TOL.  The same holds for the device and the host loop.
 """
 import json
 import os
@@ -75,20 +82,30 @@ def c4(rt):
 
 
 def check_tokens(got, f):
+    """Compares every step; returns False when the runs parted at a near
+    tie (the oracle's top-2 margin within 2 x DEEP_FP32_TOL x the step's
+    largest |logit|), True when all 527 tokens agree."""
     want = f["tokens"]
-    margins = f["margins"]
-    prompt_len = len(f["prompt"])
-    gen = margins[prompt_len - 1:]
+    margins, scales = f["margins"].astype(np.float64), f["scales"].astype(np.float64)
+    first_gen = len(f["prompt"]) - 1
+    gen = margins[first_gen:]
     print(f"c4: smallest top-2 margin over the generated steps {float(gen.min()):.3e} "
-          f"(step {prompt_len - 1 + int(gen.argmin())})", flush=True)
+          f"(step {first_gen + int(gen.argmin())})", flush=True)
     assert len(got) == len(want) == 527
     bad = np.nonzero(np.asarray(got) != want)[0]
-    if bad.size:
-        i = int(bad[0])
-        raise AssertionError(
-            f"first differing step {i} (position {i}): got {int(got[i])}, oracle {int(want[i])} "
-            f"(oracle runner-up {int(f['runners'][i])}, top-2 margin {float(margins[i]):.3e}); "
-            f"{bad.size} steps differ")
+    if bad.size == 0:
+        print("c4: all 527 tokens identical", flush=True)
+        return True
+    i = int(bad[0])
+    bound = 2 * DEEP_FP32_TOL * scales[i]
+    if i >= first_gen and margins[i] <= bound:
+        print(f"c4: tokens identical through step {i - 1}; the runs part at step {i}, a near "
+              f"tie (oracle margin {margins[i]:.3e} within {bound:.3e})", flush=True)
+        return False
+    raise AssertionError(
+        f"first differing step {i} (position {i}): got {int(got[i])}, oracle {int(want[i])} "
+        f"(oracle runner-up {int(f['runners'][i])}, top-2 margin {margins[i]:.3e} against a "
+        f"near-tie bound of {bound:.3e}); {bad.size} steps differ")
 
 
 def test_c4_device_greedy_tokens_match_oracle(c4):
@@ -97,10 +114,10 @@ def test_c4_device_greedy_tokens_match_oracle(c4):
     toks, logits, tps = model.generate_tokens_device(f["prompt"], int(f["max_new_tokens"]))
     print(f"c4 device loop: {len(toks)} tokens in {time.time() - t0:.1f} s ({tps:.1f} tok/s)",
           flush=True)
-    check_tokens(toks, f)
-    err = rel_err(logits, f["logits"])
-    print(f"c4 device loop: last-step logits rel err {err:.2e}", flush=True)
-    assert err <= DEEP_FP32_TOL
+    if check_tokens(toks, f):
+        err = rel_err(logits, f["logits"])
+        print(f"c4 device loop: last-step logits rel err {err:.2e}", flush=True)
+        assert err <= DEEP_FP32_TOL
 
 
 def test_c4_host_greedy_tokens_match_oracle(c4):
@@ -109,7 +126,7 @@ def test_c4_host_greedy_tokens_match_oracle(c4):
     toks, logits, tps = model.generate_tokens(f["prompt"], int(f["max_new_tokens"]))
     print(f"c4 host loop: {len(toks)} tokens in {time.time() - t0:.1f} s ({tps:.1f} tok/s)",
           flush=True)
-    check_tokens(toks, f)
-    err = rel_err(logits, f["logits"])
-    print(f"c4 host loop: last-step logits rel err {err:.2e}", flush=True)
-    assert err <= DEEP_FP32_TOL
+    if check_tokens(toks, f):
+        err = rel_err(logits, f["logits"])
+        print(f"c4 host loop: last-step logits rel err {err:.2e}", flush=True)
+        assert err <= DEEP_FP32_TOL

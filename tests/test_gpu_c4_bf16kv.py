@@ -32,8 +32,8 @@ earlier layers of the same step built over the same cache (the same cause,
 and so the same normwise bar, as the logits); rounding each to bf16 then
 moves an element by at most one ulp.
 
-Two phases: the 16-token prompt drawn with seed 1004 (the first seed of
-the range the fp32 fixture chose from, taken without screening) and 64
+Two phases: the 16-token prompt drawn with seed 1004 (the fp32 fixture's
+prompt, taken by rule: the first seed of its range, no screening) and 64
 greedy steps, positions 0..79; and positions 8128..8191 over a cache
 prefilled with N(0, 1) bf16 values on the device (the benchmark's cache),
 64 steps.
