@@ -360,7 +360,7 @@ AMMON_DEV void wave_lds_order() {
 //
 // LDS: att_staged_lds_floats(GMAX, NCH) floats (the merge's rows reuse the
 // chunk buffers).
-#define ATT_STAGED_OROW (ATT_MAX_HEAD + 1)  // padded merge row (bank spread)
+#define ATT_STAGED_OROW (ATT_MAX_HEAD + 4)  // merge row: 16-byte aligned, banks spread
 
 // Max / sum over lanes l and l ^ 32 (resp. l ^ 16) with gfx950's lane-swap
 // instructions (VALU, no LDS round trip): permlane32_swap(v, v) leaves the
@@ -385,7 +385,8 @@ AMMON_DEV float pair16_sum(float v) {
 constexpr uint32_t att_staged_lds_floats(int GMAX, int NCH) {
   const uint32_t ring = (uint32_t)NCH * 8192u;                      // NCH x 32 KiB
   const uint32_t merge = AMMON_WAVES * GMAX * ATT_STAGED_OROW;      // per-wave outputs
-  return (ring > merge ? ring : merge) + 2 * AMMON_WAVES * GMAX;
+  // + the waves' maxima and sums, then the workgroup's per head
+  return (ring > merge ? ring : merge) + 2 * AMMON_WAVES * GMAX + 2 * GMAX;
 }
 
 template <int GMAX, int NCH>
@@ -512,9 +513,11 @@ struct AttnPartialMfmaStaged {
   }
 
   AMMON_DEV void run(const ammon_k_attention &p, float *lds) {
-    const uint32_t ring = att_staged_lds_floats(GMAX, NCH) - 2 * AMMON_WAVES * GMAX;
+    const uint32_t ring = att_staged_lds_floats(GMAX, NCH) - 2 * AMMON_WAVES * GMAX - 2 * GMAX;
     float *s_m = lds + ring;                                       // [4][GMAX] wave maxima
     float *s_l = s_m + AMMON_WAVES * GMAX;                         // [4][GMAX] wave sums
+    float *s_M = s_l + AMMON_WAVES * GMAX;                         // [GMAX] workgroup maxima
+    float *s_L = s_M + GMAX;                                       // [GMAX] workgroup sums
     const float scale2 = 1.4426950408889634f / sqrtf((float)HEAD);  // log2(e)/sqrt(head)
     const uint32_t h = lane & 15, grp = lane >> 4;
 
@@ -654,17 +657,25 @@ struct AttnPartialMfmaStaged {
     }
     __syncthreads();
     // this wave's tiles, scaled to the workgroup max, as rows [w][h][d]
+    // (16-byte writes); wave 0 also leaves each head's max and sum
     if (h < GMAX) {
       float M = s_m[h];
 #pragma unroll
       for (int w = 1; w < AMMON_WAVES; ++w) M = fmaxf(M, s_m[w * GMAX + h]);
       // M is finite: a live split's first position is wave 0's
       const float f = __builtin_amdgcn_exp2f(m_run - M);
-      float *row = lds + (wave * GMAX + h) * ATT_STAGED_OROW + 4 * grp;
+      float4 *row = (float4 *)(lds + (wave * GMAX + h) * ATT_STAGED_OROW + 4 * grp);
 #pragma unroll
       for (int nt = 0; nt < 8; ++nt)
+        row[4 * nt] = make_float4(o[nt][0] * f, o[nt][1] * f, o[nt][2] * f, o[nt][3] * f);
+      if (wave == 0 && grp == 0) {
+        float L = 0.f;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) row[16 * nt + r] = o[nt][r] * f;
+        for (int w = 0; w < AMMON_WAVES; ++w)
+          L += s_l[w * GMAX + h] * __builtin_amdgcn_exp2f(s_m[w * GMAX + h] - M);
+        s_M[h] = M;
+        s_L[h] = L;
+      }
     }
     __syncthreads();
     const uint32_t slot_w = HEAD + 2;
@@ -673,13 +684,7 @@ struct AttnPartialMfmaStaged {
       float total = 0.f;
 #pragma unroll
       for (int w = 0; w < AMMON_WAVES; ++w) total += lds[(w * GMAX + j) * ATT_STAGED_OROW + d];
-      float M = s_m[j];
-#pragma unroll
-      for (int w = 1; w < AMMON_WAVES; ++w) M = fmaxf(M, s_m[w * GMAX + j]);
-      float L = 0.f;
-#pragma unroll
-      for (int w = 0; w < AMMON_WAVES; ++w)
-        L += s_l[w * GMAX + j] * __builtin_amdgcn_exp2f(s_m[w * GMAX + j] - M);
+      const float M = s_M[j], L = s_L[j];
       if (direct_out(p)) {  // the only split: the merge's result, total / l
         st_out(p.out + (size_t)(g * GMAX + j) * HEAD + d, total / L);
         continue;
