@@ -314,6 +314,27 @@ def test_single_split_decode_matches_two_launches(rt, kv_dtype, q_heads, kv_head
         assert rel_err(got, oracle.attention(qh, kh, vh, kv_dtype, pos)) <= RTOL, pos
 
 
+@pytest.mark.parametrize("q_heads,kv_heads", [(8, 8), (16, 8), (32, 8), (32, 4)])
+@pytest.mark.parametrize("split", [64, 128, 192])
+def test_staged_attention_every_group_size(rt, q_heads, kv_heads, split):
+    # The matrix-core unit (bf16 cache, head 128) at 1, 2, 4 and 8 q heads per
+    # kv head over several splits: one chunk per unit, two (both requested
+    # at the start) and three (the two-buffer ring refilled); positions that
+    # end mid-chunk and on a chunk boundary; dead splits must stay poisoned.
+    head, seq = 128, 1024
+    qh = oracle.normal(q_heads * head, 171).reshape(q_heads, head)
+    kh = oracle.storage(oracle.normal(seq * kv_heads * head, 172), BF16).reshape(
+        seq, kv_heads, head)
+    vh = oracle.storage(oracle.normal(seq * kv_heads * head, 173), BF16).reshape(
+        seq, kv_heads, head)
+    for pos in (1023, 700, 191, 64, 5):
+        got, part = run_attention(rt, qh, kh, vh, BF16, q_heads, kv_heads, head, seq, pos, split)
+        assert rel_err(got, oracle.attention(qh, kh, vh, BF16, pos)) <= RTOL, (pos, split)
+        live = pos // split + 1
+        assert np.all(np.isfinite(part[:, :live])), (pos, split)
+        assert np.all(np.isnan(part[:, live:])), (pos, split)
+
+
 def test_attention_partials_match_oracle_split8(rt):
     q_heads, kv_heads, head, seq, pos = 6, 6, 48, 256, 100
     qh = oracle.pseudo_random(q_heads * head, 11).reshape(q_heads, head)
