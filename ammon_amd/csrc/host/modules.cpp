@@ -213,8 +213,13 @@ void CausalAttentionBlock::record(Scheme &s, TensorView x, const CausalAttention
                                      abi(cache.key.dtype()), kv_heads, head, seq, st, split,
                                      partial);
     });
+    // the merge also brings the first tile of wo's rows into L2 for the
+    // output projection that follows
+    const void *wo = w.output.data();
+    const ammon_dtype wo_dt = abi(w.output.dtype());
     s.record("attn_combine", [=](ammon_stream stream) {
-      return ammon_attention_combine(rt, stream, partial, q_heads, head, seq, st, split, xb);
+      return ammon_attention_combine_warm(rt, stream, partial, q_heads, head, seq, st, split, xb,
+                                          wo, wo_dt, hidden, q_heads * head, 0);
     });
   }
   s.record("wo_residual", [=](ammon_stream stream) {

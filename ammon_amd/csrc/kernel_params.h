@@ -76,6 +76,13 @@ typedef struct {
                                positions the grid and scratch cover for prefill) */
   uint32_t single_out;      /* pass 1 with splits == 1 writes out (the merge's
                                result) instead of the partial; no pass 2 */
+  /* Merge only, optional (NULL: none): the next GEMV's weights.  Merge
+   * workgroup i reads one dword of every 128-byte line of row block i
+   * (rows [i warm_rows, +warm_rows), bytes [0, warm_bytes) of each, rows
+   * warm_row_bytes apart) and discards it, so the lines wait in the L2 of
+   * the XCD that runs the GEMV's workgroup i. */
+  const void *warm;
+  uint32_t warm_row_bytes, warm_rows, warm_bytes, warm_blocks;
 } ammon_k_attention;
 
 typedef struct {

@@ -737,6 +737,37 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
 #define COMB_LDS_FLOATS_W(SLICE) (COMB_SPLIT_LANES * ((SLICE) + 1) + COMB_SPLIT_LANES + AMMON_WAVES)
 #define COMB_LDS_FLOATS COMB_LDS_FLOATS_W(32)
 
+// Lines per lane of the merge's L2 warming (AMMON_WG * WARM_LINES lines, 128
+// bytes each, per workgroup at most).
+#define WARM_LINES 4
+
+// The warming loads of merge workgroup b (one dword per 128-byte line of
+// the next GEMV's row block b, see ammon_k_attention::warm).  The values
+// are kept, unused, until warm_sink at the workgroup's end, so no wait for
+// them is placed before then; they are issued after the merge's own loads,
+// and loads complete in order, so the merge's waits leave them in flight.
+// The WARM_LINES loads are issued unconditionally (with nothing to warm they
+// read as zero and touch no memory), so every path has the same count in
+// flight and the compiler's wait counts stay exact.
+AMMON_DEV void warm_issue(const ammon_k_attention &p, uint32_t b, uint32_t (&v)[WARM_LINES]) {
+  const bool on = p.warm != nullptr && b < p.warm_blocks;  // uniform
+  const uint32_t per_row = on ? p.warm_bytes / 128 : 1;
+  const uint32_t lines = on ? per_row * p.warm_rows : 0;
+  const __amdgpu_buffer_rsrc_t r = make_rsrc(
+      on ? (const char *)p.warm + (size_t)b * p.warm_rows * p.warm_row_bytes : (const char *)p.partial,
+      on ? p.warm_rows * p.warm_row_bytes : 0);
+#pragma unroll
+  for (int i = 0; i < WARM_LINES; ++i) {
+    const uint32_t l = threadIdx.x + i * AMMON_WG;
+    const uint32_t off = l < lines ? (l / per_row) * p.warm_row_bytes + (l % per_row) * 128
+                                   : AMMON_OOB;
+    v[i] = __builtin_amdgcn_raw_buffer_load_b32(r, off, 0, 0);
+  }
+}
+AMMON_DEV void warm_sink(const uint32_t (&v)[WARM_LINES]) {
+  asm volatile("" ::"v"(v[0]), "v"(v[1]), "v"(v[2]), "v"(v[3]));
+}
+
 // Unit (q head h, SLICE-dim slice) of pass 2 (SLICE 32 or 8: each lane
 // owns SLICE / 4 dims of one split lane; the per-dim arithmetic does not
 // depend on SLICE); lds holds COMB_LDS_FLOATS_W(SLICE) floats.
@@ -774,10 +805,13 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
       }
     }
   }
+  uint32_t wv[WARM_LINES];
+  warm_issue(p, blockIdx.x + gridDim.x * blockIdx.y, wv);
   const uint32_t pos = p.step->position + p.pos_add;
   if (pos >= p.limit) {
     if (threadIdx.x < SLICE && d0 + threadIdx.x < head)
       st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));
+    warm_sink(wv);
     return;
   }
   const uint32_t live = min(pos / p.split_len + 1, p.splits);
@@ -831,6 +865,7 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
     const uint32_t d = d0 + threadIdx.x;
     if (d < head) st_out(out + d, total / L);
   }
+  warm_sink(wv);
 }
 
 // The merge above for q head h by one wave (call with the whole wave).

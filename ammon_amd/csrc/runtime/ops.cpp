@@ -158,6 +158,48 @@ ammon_status gemv_pack(ammon_runtime *rt, const GemvArgs &a, const char *what, a
   return AMMON_OK;
 }
 
+// The most weight bytes a merge launch warms for the next GEMV.
+constexpr uint64_t kWarmMaxBytes = 20ull << 20;
+
+// Grid: at most gemv_wgs_per_cu resident workgroups per CU (fewer if LDS
+// bounds it); among 2..max per CU pick the count whose grid-stride split of
+// the row blocks wastes the least (blocks / (grid * blocks per workgroup)).
+uint32_t gemv_grid(ammon_runtime *rt, hipFunction_t fn, size_t lds, uint32_t row_blocks, int mode) {
+  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
+  const uint32_t resident = occupancy(rt, fn, lds);
+  const uint32_t max_per_cu = std::max<uint32_t>(1, std::min(rt->gemv_wgs_per_cu, resident));
+  uint32_t grid = std::min<uint32_t>(row_blocks, cus * max_per_cu);
+  double best = -1.0;
+  for (uint32_t w = max_per_cu; w >= 1; --w) {
+    const uint32_t g = std::min<uint32_t>(row_blocks, cus * w);
+    const uint32_t per_wg = cdiv(row_blocks, g);
+    const double eff = (double)row_blocks / ((double)g * per_wg);
+    if (eff > best + 1e-9) {
+      best = eff;
+      grid = g;
+    }
+    if (w == 1 || w <= max_per_cu / 2) break;
+  }
+  // QKV: at most two workgroups per CU, even with a ragged last round: at
+  // the Llama-3-8B shape (768 row blocks) 512 workgroups measured 10.4-10.6
+  // us against 11.5-11.6 for 768 (x requested ahead of the weights)
+  if (mode == AMMON_GEMV_QKV && max_per_cu > 2) grid = std::min<uint32_t>(row_blocks, cus * 2);
+  return grid;
+}
+
+// The grid of a RESIDUAL-mode GEMV of rows x n weights at w (its vector
+// kernel when w is 16-byte aligned and n a whole number of chunks).
+uint32_t gemv_grid_for(ammon_runtime *rt, const void *w, ammon_dtype dt, uint32_t n,
+                       uint32_t rows) {
+  const bool bf = dt == AMMON_BF16;
+  const uint32_t ch_v = bf ? 8 : 4;
+  const int vec = (n % ch_v == 0) && (((uintptr_t)w) & 15u) == 0;
+  const uint64_t tile_elems = 64ull * kGemvTileChunks * (vec ? ch_v : 1);
+  const size_t lds = (size_t)((n + tile_elems - 1) / tile_elems * tile_elems) * sizeof(float);
+  return gemv_grid(rt, rt->k.gemv[bf ? 1 : 0][vec][AMMON_GEMV_RESIDUAL], lds,
+                   cdiv(rows, kGemvRowsPerWave * kGemvWaves), AMMON_GEMV_RESIDUAL);
+}
+
 // Validates, packs and launches a GEMV; *grid_out (optional) receives the
 // workgroup count (PLAIN_ARGMAX writes one candidate per workgroup).
 ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const GemvArgs &a,
@@ -171,31 +213,10 @@ ammon_status gemv_check_and_launch(ammon_runtime *rt, ammon_stream stream, const
   size_t lds = shmem;
   // PLAIN_ARGMAX reduces the workgroup's candidates in x's LDS
   if (a.mode == AMMON_GEMV_PLAIN_ARGMAX) lds = std::max<size_t>(lds, 2 * kWorkgroup * 4);
-  // Grid: at most gemv_wgs_per_cu resident workgroups per CU (fewer if LDS
-  // bounds it); among 2..max per CU pick the count whose grid-stride split of
-  // the row blocks wastes the least (blocks / (grid * blocks per workgroup)).
-  const uint32_t cus = (uint32_t)std::max(rt->info.compute_units, 1);
   hipFunction_t fn = gemv_wide(a, vec)                  ? rt->k.gemv_wide[a.mode == AMMON_GEMV_PLAIN_ARGMAX]
                      : a.mode == AMMON_GEMV_PLAIN_ARGMAX ? rt->k.gemv_argmax[dt][vec]
                                                          : rt->k.gemv[dt][vec][a.mode];
-  const uint32_t resident = occupancy(rt, fn, lds);
-  const uint32_t max_per_cu = std::max<uint32_t>(1, std::min(rt->gemv_wgs_per_cu, resident));
-  uint32_t grid = std::min<uint32_t>(p.row_blocks, cus * max_per_cu);
-  double best = -1.0;
-  for (uint32_t w = max_per_cu; w >= 1; --w) {
-    const uint32_t g = std::min<uint32_t>(p.row_blocks, cus * w);
-    const uint32_t per_wg = cdiv(p.row_blocks, g);
-    const double eff = (double)p.row_blocks / ((double)g * per_wg);
-    if (eff > best + 1e-9) {
-      best = eff;
-      grid = g;
-    }
-    if (w == 1 || w <= max_per_cu / 2) break;
-  }
-  // QKV: at most two workgroups per CU, even with a ragged last round: at
-  // the Llama-3-8B shape (768 row blocks) 512 workgroups measured 10.4-10.6
-  // us against 11.5-11.6 for 768 (x requested ahead of the weights)
-  if (a.mode == AMMON_GEMV_QKV && max_per_cu > 2) grid = std::min<uint32_t>(p.row_blocks, cus * 2);
+  uint32_t grid = gemv_grid(rt, fn, lds, p.row_blocks, a.mode);
   if (a.mode == AMMON_GEMV_PLAIN_ARGMAX)
     AMMON_CHECK(grid <= a.cand_cap, "%s: scratch holds %u candidates, the launch needs %u", what,
                 a.cand_cap, grid);
@@ -403,7 +424,7 @@ ammon_status attention_pass1(ammon_runtime *rt, ammon_stream stream, const float
   const uint32_t splits = ammon_attention_splits(seq, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, single_out,
                          q_heads, kv_heads, head, seq, split_len, splits, 0, seq,
-                         single_out ? 1u : 0u};
+                         single_out ? 1u : 0u, nullptr, 0, 0, 0, 0};
   return launch_att(rt, stream, f, splits, kv_heads, 1, p, "attention_partial");
 }
 }  // namespace
@@ -424,6 +445,16 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
                                      const float *partial, uint32_t q_heads, uint32_t head,
                                      uint32_t seq, const ammon_decode_step *step,
                                      uint32_t split_len, float *out) {
+  return ammon_attention_combine_warm(rt, stream, partial, q_heads, head, seq, step, split_len,
+                                      out, nullptr, AMMON_BF16, 0, 0, 0);
+}
+
+ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream,
+                                          const float *partial, uint32_t q_heads, uint32_t head,
+                                          uint32_t seq, const ammon_decode_step *step,
+                                          uint32_t split_len, float *out, const void *next_w,
+                                          ammon_dtype next_dtype, uint32_t next_rows,
+                                          uint32_t next_n, uint32_t warm_row_bytes) {
   REQUIRE_RT();
   AMMON_CHECK(partial && step && out, "attention_combine: NULL partial, step or out");
   AMMON_CHECK(q_heads > 0 && head > 0 && seq > 0,
@@ -439,7 +470,39 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
-                         ammon_attention_splits(seq, split_len), 0, seq, 0};
+                         ammon_attention_splits(seq, split_len), 0, seq, 0, nullptr, 0, 0, 0, 0};
+  const uint32_t grid = q_heads * cdiv(head, 8);
+  if (next_w) {
+    AMMON_CHECK(valid_dtype(next_dtype), "attention_combine: unknown next weight dtype %d",
+                (int)next_dtype);
+    AMMON_CHECK(next_rows > 0 && next_n > 0, "attention_combine: empty next matrix (%u x %u)",
+                next_rows, next_n);
+    // The next GEMV (a RESIDUAL-mode ammon_gemv of next_rows x next_n) gives
+    // row block j (kGemvRowsPerWave * kGemvWaves rows) to workgroup j % its
+    // grid, which runs on XCD (j % grid) % 8, and requests each row's first
+    // tile (64 lanes x kGemvTileChunks x 16 bytes) first; merge workgroup i
+    // runs on XCD i % 8.  So merge workgroup i warms block i when every block
+    // has a workgroup of its own and both grids are whole multiples of the 8
+    // XCDs.  Warming half a tile bought nothing when measured (a wave waits
+    // for the slowest of its loads), and more than ~20 MB overflows the 8
+    // XCDs' 4 MB L2s.
+    const uint64_t row_bytes = (uint64_t)next_n * dsize(next_dtype);
+    const uint32_t rows_per_wg = kGemvRowsPerWave * kGemvWaves;
+    const uint32_t blocks = cdiv(next_rows, rows_per_wg);
+    const uint32_t gemv_grid = gemv_grid_for(rt, next_w, next_dtype, next_n, next_rows);
+    const uint64_t want = warm_row_bytes ? warm_row_bytes : 64ull * kGemvTileChunks * 16;
+    const uint64_t bytes = std::min<uint64_t>(want, row_bytes) / 128 * 128;
+    if (gemv_grid % 8 == 0 && grid % 8 == 0 && blocks == gemv_grid && blocks <= grid &&
+        bytes > 0 && (uint64_t)rows_per_wg * row_bytes < (1ull << 31) &&
+        bytes / 128 * rows_per_wg <= (uint64_t)kWorkgroup * 4 &&
+        (uint64_t)blocks * rows_per_wg * bytes <= kWarmMaxBytes) {
+      p.warm = next_w;
+      p.warm_row_bytes = (uint32_t)row_bytes;
+      p.warm_rows = rows_per_wg;
+      p.warm_bytes = (uint32_t)bytes;
+      p.warm_blocks = blocks;
+    }
+  }
   return launch_att(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 8), 1, p,
                     "attention_combine");
 }
@@ -535,7 +598,7 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
   // out-of-range treatment -- NaN output, no partial -- like one past seq
   const uint32_t splits = ammon_attention_splits(ctx, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, out,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx, 0};
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx, 0, nullptr, 0, 0, 0, 0};
   st = launch_att(rt, stream, f, splits, kv_heads, tokens, p, "attention_prefill");
   if (st != AMMON_OK) return st;
   return launch_att(rt, stream, rt->k.att_combine_waves, cdiv(q_heads, kWaves), 1, tokens, p,

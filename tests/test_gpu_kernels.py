@@ -335,6 +335,53 @@ def test_staged_attention_every_group_size(rt, q_heads, kv_heads, split):
         assert np.all(np.isnan(part[:, live:])), (pos, split)
 
 
+def test_combine_warm_matches_combine(rt):
+    # ammon_attention_combine_warm merges exactly as ammon_attention_combine
+    # (bit for bit) whether it warms the next GEMV's rows (the Llama-3-8B wo,
+    # 4096 x 4096 bf16: one row block per workgroup), warms whole rows, or
+    # skips warming (a matrix whose blocks do not line up with the merge
+    # grid, no matrix); a bad next matrix is a validation error.
+    q_heads, kv_heads, head, seq, split = 32, 8, 128, 2048, 128
+    qh = oracle.normal(q_heads * head, 181).reshape(q_heads, head)
+    kh = oracle.storage(oracle.normal(seq * kv_heads * head, 182), BF16).reshape(
+        seq, kv_heads, head)
+    vh = oracle.storage(oracle.normal(seq * kv_heads * head, 183), BF16).reshape(
+        seq, kv_heads, head)
+    q = up(rt, qh)
+    kc, vc = up(rt, head_major(kh, kv_heads, seq, head)), up(rt, head_major(vh, kv_heads, seq, head))
+    splits = -(-seq // split)
+    part = rt.alloc(q_heads * splits * (head + 2) * 4)
+    plain, warm = rt.alloc(q_heads * head * 4), rt.alloc(q_heads * head * 4)
+    dim = q_heads * head
+    wo = rt.alloc(dim * dim * 2)
+    rt.fill_normal(wo, BF16, dim * dim, 184, 0, 0.0, 0.02)
+    step = rt.step(0, 0)
+    for pos in (2047, 1000, 130):
+        rt.deposit(step, 0, pos)
+        call("ammon_attention_partial", rt.handle, None, q, q_heads, kc, vc, BF16, kv_heads,
+             head, seq, step, split, part)
+        call("ammon_attention_combine", rt.handle, None, part, q_heads, head, seq, step, split,
+             plain)
+        want = down(plain, (q_heads, head))
+        assert rel_err(want, oracle.attention(qh, kh, vh, BF16, pos)) <= RTOL, pos
+        for nxt, rows, n, row_bytes in ((wo, dim, dim, 0), (wo, dim, dim, 2 * dim),
+                                        (wo, 100, dim, 0), (None, 0, 0, 0)):
+            rt.fill(warm, F32, q_heads * head, float("nan"))
+            call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
+                 split, warm, nxt, BF16, rows, n, row_bytes)
+            got = down(warm, (q_heads, head))
+            np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32),
+                                          err_msg=f"pos {pos} rows {rows} bytes {row_bytes}")
+    with pytest.raises(AmmonError):
+        call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
+             split, warm, wo, 7, dim, dim, 0)
+    with pytest.raises(AmmonError):
+        call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
+             split, warm, wo, BF16, 0, dim, 0)
+    rt.synchronize()
+    wo.free()
+
+
 def test_attention_partials_match_oracle_split8(rt):
     q_heads, kv_heads, head, seq, pos = 6, 6, 48, 256, 100
     qh = oracle.pseudo_random(q_heads * head, 11).reshape(q_heads, head)
