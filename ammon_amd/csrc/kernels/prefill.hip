@@ -707,20 +707,24 @@ AMMON_DEV void gemm_big(const ammon_k_gemm &p) {
 GEMM_MODES(bf16, uint16_t, 512)
 GEMM_MODES(f32, float, 256)
 
-// long prompts, bf16 W: 16 NT-token tiles, RT 16-row tiles per wave
-#define GEMM_BIG_KERNEL(NAME, MODE, RT, NT)                                        \
-  extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(ammon_k_gemm p) { \
-    gemm_big<MODE, RT, NT>(p);                                                   \
+// long prompts, bf16 W: 16 NT-token tiles, RT 16-row tiles per wave.  OCC:
+// workgroups per CU the registers must allow (the LDS allows 2 of the
+// 64-token tiles' 72 KiB, 4 of the 32-token tiles' 36 KiB); left to itself
+// the compiler gave the 64-row-per-wave tiles 288 registers (one wave per
+// SIMD) and shuffled the SwiGLU tile's accumulators between register files.
+#define GEMM_BIG_KERNEL(NAME, MODE, RT, NT, OCC)                                        \
+  extern "C" __global__ __launch_bounds__(AMMON_WG, OCC) void NAME(ammon_k_gemm p) { \
+    gemm_big<MODE, RT, NT>(p);                                                        \
   }
-#define GEMM_BIG_MODES(SUFFIX, RT, NT)                                                 \
-  GEMM_BIG_KERNEL(ammon_gemm_bf16_plain_##SUFFIX, AMMON_GEMV_PLAIN, RT, NT)            \
-  GEMM_BIG_KERNEL(ammon_gemm_bf16_residual_##SUFFIX, AMMON_GEMV_RESIDUAL, RT, NT)      \
-  GEMM_BIG_KERNEL(ammon_gemm_bf16_swiglu_##SUFFIX, AMMON_GEMV_SWIGLU, RT, NT)          \
-  GEMM_BIG_KERNEL(ammon_gemm_bf16_qkv_##SUFFIX, AMMON_GEMV_QKV, RT, NT)
-GEMM_BIG_MODES(t64_r4, 4, 4)
-GEMM_BIG_MODES(t64_r2, 2, 4)
-GEMM_BIG_MODES(t32_r4, 4, 2)
-GEMM_BIG_MODES(t32_r2, 2, 2)
+#define GEMM_BIG_MODES(SUFFIX, RT, NT, OCC)                                                 \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_plain_##SUFFIX, AMMON_GEMV_PLAIN, RT, NT, OCC)            \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_residual_##SUFFIX, AMMON_GEMV_RESIDUAL, RT, NT, OCC)      \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_swiglu_##SUFFIX, AMMON_GEMV_SWIGLU, RT, NT, OCC)          \
+  GEMM_BIG_KERNEL(ammon_gemm_bf16_qkv_##SUFFIX, AMMON_GEMV_QKV, RT, NT, OCC)
+GEMM_BIG_MODES(t64_r4, 4, 4, 2)
+GEMM_BIG_MODES(t64_r2, 2, 4, 2)
+GEMM_BIG_MODES(t32_r4, 4, 2, 2)
+GEMM_BIG_MODES(t32_r2, 2, 2, 4)
 
 // y[t][r] = (residual[t][r] +) the split ranges' partial sums added in range
 // order: grid-stride over tokens x d.
