@@ -13,6 +13,10 @@
 #define ATT_KERNEL(NAME) \
   extern "C" __global__ __launch_bounds__(AMMON_WG) void NAME(const ammon_k_step *step, \
                                                              ammon_k_attention p_)
+// ... with registers for at least OCC workgroups per CU
+#define ATT_KERNEL_OCC(NAME, OCC)                                                           \
+  extern "C" __global__ __launch_bounds__(AMMON_WG, OCC) void NAME(const ammon_k_step *step, \
+                                                                  ammon_k_attention p_)
 #define ATT_PARAMS(p0)     \
   ammon_k_attention p0 = p_; \
   p0.step = step
@@ -55,8 +59,11 @@ ATT_PARTIAL_H128(ammon_attention_partial_h128_f32_c4, float, 4)
 
 // bf16 K/V, head 128: K/V staged in an LDS ring of NCH 64-position chunk
 // buffers by 16-byte buffer-to-LDS requests (AttnPartialMfmaStaged)
+// (two per CU, as the two-buffer ring's LDS allows: left to itself the
+// compiler put the score tiles in the accumulator registers and copied them
+// out: 192 copy instructions in the 4:1 kernel)
 #define ATT_PARTIAL_STAGED(NAME, GMAX, NCH)                                          \
-  ATT_KERNEL(NAME) {                                                                \
+  ATT_KERNEL_OCC(NAME, 2) {                                                         \
     ATT_PARAMS(p0);                                                                 \
     __shared__ float lds[att_staged_lds_floats(GMAX, NCH)];                         \
     const ammon_k_attention p = attention_token(p0, blockIdx.z);                    \
