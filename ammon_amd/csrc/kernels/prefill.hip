@@ -641,14 +641,23 @@ AMMON_DEV void gemm_big(const ammon_k_gemm &p) {
   // (x0..x2), LDS buffer ch % 3
   u32x4 a0[RT], a1[RT], a2[RT], a3[RT], a4[RT], a5[RT];
   u32x4 x0[T::XU][2], x1[T::XU][2], x2[T::XU][2];
+  // issue order pinned as the loop's (see below)
   tile.load_w(0, a0);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_w(1, a1);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_x(0, x0);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_w(2, a2);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_w(3, a3);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_x(1, x1);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_w(4, a4);
+  __builtin_amdgcn_sched_barrier(0);
   tile.load_w(5, a5);
+  __builtin_amdgcn_sched_barrier(0);
   // Chunk c: stage its x (loaded two chunks ago) into LDS buffer c % 3,
   // then request x of chunk c + 2 and, as each step's W is used, the W six
   // steps on.  Buffer c % 3 was last read for chunk c - 3, which every wave
