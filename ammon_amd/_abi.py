@@ -91,7 +91,7 @@ SIGNATURES = {
                                       _U32, _P]),
     "ammon_attention_combine": (_ST, [_P, _P, _P, _U32, _U32, _U32, _P, _U32, _P]),
     "ammon_attention_combine_warm": (_ST, [_P, _P, _P, _U32, _U32, _U32, _P, _U32, _P, _P, _DT,
-                                           _U32, _U32, _U32]),
+                                           _U32, _U32, _U32, _U32]),
     "ammon_attention_decode": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _U32, _P,
                                      _U32, _P, _SZ, _P]),
     "ammon_attention_decode_noalloc": (_ST, [_P, _P, _P, _U32, _P, _P, _DT, _U32, _U32, _U32,

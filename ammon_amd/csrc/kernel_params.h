@@ -80,9 +80,10 @@ typedef struct {
    * workgroup i reads one dword of every 128-byte line of row block i
    * (rows [i warm_rows, +warm_rows), bytes [0, warm_bytes) of each, rows
    * warm_row_bytes apart) and discards it, so the lines wait in the L2 of
-   * the XCD that runs the GEMV's workgroup i. */
+   * the XCD that runs the GEMV's workgroup i; only at positions of at
+   * least warm_min_pos. */
   const void *warm;
-  uint32_t warm_row_bytes, warm_rows, warm_bytes, warm_blocks;
+  uint32_t warm_row_bytes, warm_rows, warm_bytes, warm_blocks, warm_min_pos;
 } ammon_k_attention;
 
 typedef struct {

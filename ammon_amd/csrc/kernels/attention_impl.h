@@ -749,8 +749,9 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
 // The WARM_LINES loads are issued unconditionally (with nothing to warm they
 // read as zero and touch no memory), so every path has the same count in
 // flight and the compiler's wait counts stay exact.
-AMMON_DEV void warm_issue(const ammon_k_attention &p, uint32_t b, uint32_t (&v)[WARM_LINES]) {
-  const bool on = p.warm != nullptr && b < p.warm_blocks;  // uniform
+AMMON_DEV void warm_issue(const ammon_k_attention &p, uint32_t b, uint32_t pos,
+                          uint32_t (&v)[WARM_LINES]) {
+  const bool on = p.warm != nullptr && b < p.warm_blocks && pos >= p.warm_min_pos;  // uniform
   const uint32_t per_row = on ? p.warm_bytes / 128 : 1;
   const uint32_t lines = on ? per_row * p.warm_rows : 0;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(
@@ -805,9 +806,9 @@ AMMON_DEV void attention_combine_unit(const ammon_k_attention &p, uint32_t h, ui
       }
     }
   }
-  uint32_t wv[WARM_LINES];
-  warm_issue(p, blockIdx.x + gridDim.x * blockIdx.y, wv);
   const uint32_t pos = p.step->position + p.pos_add;
+  uint32_t wv[WARM_LINES];
+  warm_issue(p, blockIdx.x + gridDim.x * blockIdx.y, pos, wv);
   if (pos >= p.limit) {
     if (threadIdx.x < SLICE && d0 + threadIdx.x < head)
       st_out(out + d0 + threadIdx.x, __uint_as_float(0x7fc00000u));

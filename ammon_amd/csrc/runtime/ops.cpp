@@ -424,7 +424,7 @@ ammon_status attention_pass1(ammon_runtime *rt, ammon_stream stream, const float
   const uint32_t splits = ammon_attention_splits(seq, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, single_out,
                          q_heads, kv_heads, head, seq, split_len, splits, 0, seq,
-                         single_out ? 1u : 0u, nullptr, 0, 0, 0, 0};
+                         single_out ? 1u : 0u, nullptr, 0, 0, 0, 0, 0};
   return launch_att(rt, stream, f, splits, kv_heads, 1, p, "attention_partial");
 }
 }  // namespace
@@ -446,7 +446,7 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
                                      uint32_t seq, const ammon_decode_step *step,
                                      uint32_t split_len, float *out) {
   return ammon_attention_combine_warm(rt, stream, partial, q_heads, head, seq, step, split_len,
-                                      out, nullptr, AMMON_BF16, 0, 0, 0);
+                                      out, nullptr, AMMON_BF16, 0, 0, 0, 0);
 }
 
 ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream,
@@ -454,7 +454,8 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
                                           uint32_t seq, const ammon_decode_step *step,
                                           uint32_t split_len, float *out, const void *next_w,
                                           ammon_dtype next_dtype, uint32_t next_rows,
-                                          uint32_t next_n, uint32_t warm_row_bytes) {
+                                          uint32_t next_n, uint32_t warm_row_bytes,
+                                          uint32_t min_position) {
   REQUIRE_RT();
   AMMON_CHECK(partial && step && out, "attention_combine: NULL partial, step or out");
   AMMON_CHECK(q_heads > 0 && head > 0 && seq > 0,
@@ -470,7 +471,7 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
-                         ammon_attention_splits(seq, split_len), 0, seq, 0, nullptr, 0, 0, 0, 0};
+                         ammon_attention_splits(seq, split_len), 0, seq, 0, nullptr, 0, 0, 0, 0, 0};
   const uint32_t grid = q_heads * cdiv(head, 8);
   if (next_w) {
     AMMON_CHECK(valid_dtype(next_dtype), "attention_combine: unknown next weight dtype %d",
@@ -501,6 +502,7 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
       p.warm_rows = rows_per_wg;
       p.warm_bytes = (uint32_t)bytes;
       p.warm_blocks = blocks;
+      p.warm_min_pos = min_position;
     }
   }
   return launch_att(rt, stream, rt->k.att_combine, q_heads, cdiv(head, 8), 1, p,
@@ -598,7 +600,7 @@ ammon_status ammon_attention_prefill(ammon_runtime *rt, ammon_stream stream, con
   // out-of-range treatment -- NaN output, no partial -- like one past seq
   const uint32_t splits = ammon_attention_splits(ctx, split_len);
   ammon_k_attention p = {q, k_cache, v_cache, (const ammon_k_step *)step, partial, out,
-                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx, 0, nullptr, 0, 0, 0, 0};
+                         q_heads, kv_heads, head, seq, split_len, splits, 0, ctx, 0, nullptr, 0, 0, 0, 0, 0};
   st = launch_att(rt, stream, f, splits, kv_heads, tokens, p, "attention_prefill");
   if (st != AMMON_OK) return st;
   return launch_att(rt, stream, rt->k.att_combine_waves, cdiv(q_heads, kWaves), 1, tokens, p,

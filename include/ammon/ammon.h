@@ -246,16 +246,19 @@ ammon_status ammon_attention_combine(ammon_runtime *rt, ammon_stream stream,
  * projection that consumes out -- into the L2 of the XCD whose workgroup of
  * that GEMV (a RESIDUAL-mode ammon_gemv) reads them first; warm_row_bytes 0
  * means the GEMV's first tile of each row (4 KiB), next_w NULL no warming.
- * out is bit-identical to ammon_attention_combine's.  Warming is skipped
- * where the two launches' workgroup-to-XCD maps do not line up or the bytes
- * would overflow the L2s.  No counterpart in the reference (its combine and
+ * The warming happens only at step->position >= min_position (it paid at
+ * 4096 positions and beyond and cost time at 2048 and below).  out is
+ * bit-identical to ammon_attention_combine's.  Warming is skipped where
+ * the two launches' workgroup-to-XCD maps do not line up or the bytes would
+ * overflow the L2s.  No counterpart in the reference (its combine and
  * matmul are separate launches with no such hand-over). */
 ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream,
                                           const float *partial, uint32_t q_heads, uint32_t head,
                                           uint32_t seq, const ammon_decode_step *step,
                                           uint32_t split_len, float *out, const void *next_w,
                                           ammon_dtype next_dtype, uint32_t next_rows,
-                                          uint32_t next_n, uint32_t warm_row_bytes);
+                                          uint32_t next_n, uint32_t warm_row_bytes,
+                                          uint32_t min_position);
 /* Both passes (the reference's attn_partial + attn_combine pair,
  * src/blocks.rs:240-253).  When one split covers the cache
  * (ammon_attention_splits(seq, split_len) == 1) it is one launch: pass 1

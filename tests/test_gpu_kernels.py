@@ -339,8 +339,9 @@ def test_combine_warm_matches_combine(rt):
     # ammon_attention_combine_warm merges exactly as ammon_attention_combine
     # (bit for bit) whether it warms the next GEMV's rows (the Llama-3-8B wo,
     # 4096 x 4096 bf16: one row block per workgroup), warms whole rows, or
-    # skips warming (a matrix whose blocks do not line up with the merge
-    # grid, no matrix); a bad next matrix is a validation error.
+    # skips warming (a position below the threshold, a matrix whose blocks
+    # do not line up with the merge grid, no matrix); a bad next matrix is a
+    # validation error.
     q_heads, kv_heads, head, seq, split = 32, 8, 128, 2048, 128
     qh = oracle.normal(q_heads * head, 181).reshape(q_heads, head)
     kh = oracle.storage(oracle.normal(seq * kv_heads * head, 182), BF16).reshape(
@@ -368,16 +369,16 @@ def test_combine_warm_matches_combine(rt):
                                         (wo, 100, dim, 0), (None, 0, 0, 0)):
             rt.fill(warm, F32, q_heads * head, float("nan"))
             call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
-                 split, warm, nxt, BF16, rows, n, row_bytes)
+                 split, warm, nxt, BF16, rows, n, row_bytes, 1024)
             got = down(warm, (q_heads, head))
             np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32),
                                           err_msg=f"pos {pos} rows {rows} bytes {row_bytes}")
     with pytest.raises(AmmonError):
         call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
-             split, warm, wo, 7, dim, dim, 0)
+             split, warm, wo, 7, dim, dim, 0, 0)
     with pytest.raises(AmmonError):
         call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
-             split, warm, wo, BF16, 0, dim, 0)
+             split, warm, wo, BF16, 0, dim, 0, 0)
     rt.synchronize()
     wo.free()
 
