@@ -188,13 +188,15 @@ uint32_t gemv_grid(ammon_runtime *rt, hipFunction_t fn, size_t lds, uint32_t row
 }
 
 // The grid of a RESIDUAL-mode GEMV of rows x n weights at w (its vector
-// kernel when w is 16-byte aligned and n a whole number of chunks).
+// kernel when w is 16-byte aligned and n a whole number of chunks) and, in
+// *tile_row_bytes, the bytes of each row its first tile covers.
 uint32_t gemv_grid_for(ammon_runtime *rt, const void *w, ammon_dtype dt, uint32_t n,
-                       uint32_t rows) {
+                       uint32_t rows, uint64_t *tile_row_bytes) {
   const bool bf = dt == AMMON_BF16;
   const uint32_t ch_v = bf ? 8 : 4;
   const int vec = (n % ch_v == 0) && (((uintptr_t)w) & 15u) == 0;
   const uint64_t tile_elems = 64ull * kGemvTileChunks * (vec ? ch_v : 1);
+  *tile_row_bytes = tile_elems * dsize(dt);
   const size_t lds = (size_t)((n + tile_elems - 1) / tile_elems * tile_elems) * sizeof(float);
   return gemv_grid(rt, rt->k.gemv[bf ? 1 : 0][vec][AMMON_GEMV_RESIDUAL], lds,
                    cdiv(rows, kGemvRowsPerWave * kGemvWaves), AMMON_GEMV_RESIDUAL);
@@ -481,7 +483,7 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
     // The next GEMV (a RESIDUAL-mode ammon_gemv of next_rows x next_n) gives
     // row block j (kGemvRowsPerWave * kGemvWaves rows) to workgroup j % its
     // grid, which runs on XCD (j % grid) % 8, and requests each row's first
-    // tile (64 lanes x kGemvTileChunks x 16 bytes) first; merge workgroup i
+    // tile (64 lanes x kGemvTileChunks chunks) first; merge workgroup i
     // runs on XCD i % 8.  So merge workgroup i warms block i when every block
     // has a workgroup of its own and both grids are whole multiples of the 8
     // XCDs.  Warming half a tile bought nothing when measured (a wave waits
@@ -490,8 +492,10 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
     const uint64_t row_bytes = (uint64_t)next_n * dsize(next_dtype);
     const uint32_t rows_per_wg = kGemvRowsPerWave * kGemvWaves;
     const uint32_t blocks = cdiv(next_rows, rows_per_wg);
-    const uint32_t gemv_grid = gemv_grid_for(rt, next_w, next_dtype, next_n, next_rows);
-    const uint64_t want = warm_row_bytes ? warm_row_bytes : 64ull * kGemvTileChunks * 16;
+    uint64_t tile_row_bytes = 0;
+    const uint32_t gemv_grid =
+        gemv_grid_for(rt, next_w, next_dtype, next_n, next_rows, &tile_row_bytes);
+    const uint64_t want = warm_row_bytes ? warm_row_bytes : tile_row_bytes;
     const uint64_t bytes = std::min<uint64_t>(want, row_bytes) / 128 * 128;
     if (gemv_grid % 8 == 0 && grid % 8 == 0 && blocks == gemv_grid && blocks <= grid &&
         bytes > 0 && (uint64_t)rows_per_wg * row_bytes < (1ull << 31) &&
