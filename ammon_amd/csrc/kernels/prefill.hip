@@ -141,17 +141,18 @@ struct GemmTile {
   }
 
   // x unit u = tid + 256 m of chunk `ch` (8 consecutive k of one token):
-  // the 64 units of each group u / 64 are one (step, column tile) B fragment
-  // in lane order, so a wave stages a contiguous 1 KiB of LDS per part (no
-  // bank conflicts); tokens and k past the end read as zero (no branches).
+  // the 64 units of each group u / 64 are 8 tokens x 8 consecutive k groups,
+  // so a wave's loads read 8 rows of x, 256 contiguous bytes each; the unit
+  // is B-fragment lane l = t % 16 + 16 (kg % 4) of step kg / 4 and column
+  // tile t / 16.  Tokens and k past the end read as zero (no branches).
   AMMON_DEV static void unit(uint32_t u, uint32_t &s, uint32_t &c, uint32_t &l, uint32_t &t,
                              uint32_t &kg) {
-    const uint32_t g = u >> 6;
-    l = u & 63;
-    c = g % NT;
-    s = g / NT;
-    t = 16 * c + (l & 15);
-    kg = 4 * s + (l >> 4);
+    const uint32_t g = u >> 6, ln = u & 63;
+    t = 8 * (g % (TB / 8)) + (ln >> 3);
+    kg = 8 * (g / (TB / 8)) + (ln & 7);
+    s = kg >> 2;
+    c = t >> 4;
+    l = (t & 15) + 16 * (kg & 3);
   }
 
   AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[XU][2]) const {
@@ -167,8 +168,12 @@ struct GemmTile {
     }
   }
 
+  // LDS slot of B-fragment lane l of (step s, column tile c, part q), lanes
+  // XOR-swizzled within their 16-quad row as in BigTile::quad (conflict-free
+  // operand reads and staging writes).
   AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
-    return ((s * NT + c) * XQ + q) * 64 + l;
+    const uint32_t pos = (((l & 15) ^ (4 * (l >> 4)) ^ (2 * s)) & 15) | (l & 48);
+    return ((s * NT + c) * XQ + q) * 64 + pos;
   }
 
   // Split / pack the x chunk into LDS in B-operand order.
@@ -498,16 +503,19 @@ struct BigTile {
   }
 
   // x unit u (8 consecutive k of one token) of a chunk: the 64 units of
-  // each group u / 64 are one (step, column tile) B fragment in lane order,
-  // so a wave stages a contiguous 1 KiB of LDS per part (no bank conflicts).
+  // each group u / 64 are 8 tokens x the chunk's 8 k groups, so each wave's
+  // two 16-byte loads per unit cover 8 rows of x, 256 contiguous bytes each
+  // (B-fragment order, 16 tokens x 4 k groups per load, made the 512-token
+  // gate/up GEMM 15% slower); the unit is B-fragment lane l = t % 16 +
+  // 16 (kg % 4) of step kg / 4 and column tile t / 16.
   AMMON_DEV static void unit(uint32_t u, uint32_t &s, uint32_t &c, uint32_t &l, uint32_t &t,
                              uint32_t &kg) {
-    const uint32_t g = u >> 6;
-    l = u & 63;
-    c = g % NT;
-    s = g / NT;
-    t = 16 * c + (l & 15);
-    kg = 4 * s + (l >> 4);
+    const uint32_t g = u >> 6, ln = u & 63;
+    t = 8 * g + (ln >> 3);
+    kg = ln & 7;
+    s = kg >> 2;
+    c = t >> 4;
+    l = (t & 15) + 16 * (kg & 3);
   }
 
   AMMON_DEV void load_x(uint32_t ch, u32x4 (&x)[XU][2]) const {
@@ -524,8 +532,14 @@ struct BigTile {
     }
   }
 
+  // LDS slot of B-fragment lane l of (step s, column tile c, part q): the
+  // fragment's 64 quads, with lane l's position within its 16-quad row
+  // XOR-swizzled by its k group and the step, so the operand reads (16
+  // consecutive lanes) and the staging writes (2 tokens x 8 k groups) each
+  // fall on 16 distinct 16-byte bank groups.
   AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
-    return ((s * NT + c) * 3 + q) * 64 + l;
+    const uint32_t pos = (((l & 15) ^ (4 * (l >> 4)) ^ (2 * s)) & 15) | (l & 48);
+    return ((s * NT + c) * 3 + q) * 64 + pos;
   }
 
   AMMON_DEV void stage(const u32x4 (&x)[XU][2], u32x4 *xs) const {
