@@ -169,10 +169,10 @@ struct GemmTile {
   }
 
   // LDS slot of B-fragment lane l of (step s, column tile c, part q), lanes
-  // XOR-swizzled within their 16-quad row as in BigTile::quad (conflict-free
-  // operand reads and staging writes).
+  // XOR-swizzled within their 16-quad row as in BigTile::quad below
+  // (conflict-free operand reads and staging writes).
   AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
-    const uint32_t pos = (((l & 15) ^ (4 * (l >> 4)) ^ (2 * s)) & 15) | (l & 48);
+    const uint32_t pos = (((l & 15) ^ ((l >> 4) | 4 * (s & 1))) & 15) | (l & 48);
     return ((s * NT + c) * XQ + q) * 64 + pos;
   }
 
@@ -534,11 +534,14 @@ struct BigTile {
 
   // LDS slot of B-fragment lane l of (step s, column tile c, part q): the
   // fragment's 64 quads, with lane l's position within its 16-quad row
-  // XOR-swizzled by its k group and the step, so the operand reads (16
-  // consecutive lanes) and the staging writes (2 tokens x 8 k groups) each
-  // fall on 16 distinct 16-byte bank groups.
+  // XOR-swizzled by its k group and the step's parity.  LDS serves a
+  // 16-byte access 8 lanes (128 bytes) at a time: the operand reads' 8
+  // lanes stay within one 8-quad run, and a staging write's 8 lanes (one
+  // token, 8 k groups over two steps) get the 8 distinct values of
+  // (k group | 4 (step & 1)) in the low three bits, so neither conflicts
+  // (an XOR by 4 (k group) ^ 2 step left the writes 2-way conflicted).
   AMMON_DEV static uint32_t quad(uint32_t s, uint32_t c, uint32_t q, uint32_t l) {
-    const uint32_t pos = (((l & 15) ^ (4 * (l >> 4)) ^ (2 * s)) & 15) | (l & 48);
+    const uint32_t pos = (((l & 15) ^ ((l >> 4) | 4 * (s & 1))) & 15) | (l & 48);
     return ((s * NT + c) * 3 + q) * 64 + pos;
   }
 
