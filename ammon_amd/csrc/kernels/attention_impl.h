@@ -751,7 +751,10 @@ AMMON_DEV ammon_k_attention attention_token(const ammon_k_attention &p, uint32_t
 // flight and the compiler's wait counts stay exact.
 AMMON_DEV void warm_issue(const ammon_k_attention &p, uint32_t b, uint32_t pos,
                           uint32_t (&v)[WARM_LINES]) {
-  const bool on = p.warm != nullptr && b < p.warm_blocks && pos >= p.warm_min_pos;  // uniform
+  // (not when the merge streams its partials after this point: its waits
+  // would then wait for these loads too)
+  const bool on = p.warm != nullptr && b < p.warm_blocks && pos >= p.warm_min_pos &&
+                  p.splits <= COMB_ROUNDS * COMB_SPLIT_LANES;  // uniform
   const uint32_t per_row = on ? p.warm_bytes / 128 : 1;
   const uint32_t lines = on ? per_row * p.warm_rows : 0;
   const __amdgpu_buffer_rsrc_t r = make_rsrc(
