@@ -470,16 +470,18 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
   AMMON_CHECK(ammon_attention_splits(seq, split_len) <= AMMON_ATTENTION_MAX_SPLITS,
               "attention_combine: %u splits exceed %u", ammon_attention_splits(seq, split_len),
               AMMON_ATTENTION_MAX_SPLITS);
+  if (next_w) {
+    AMMON_CHECK(valid_dtype(next_dtype), "attention_combine: unknown next weight dtype %d",
+                (int)next_dtype);
+    AMMON_CHECK(next_rows > 0 && next_n > 0, "attention_combine: empty next matrix (%u x %u)",
+                next_rows, next_n);
+  }
   VALIDATE_ONLY();
   ammon_k_attention p = {nullptr, nullptr, nullptr, (const ammon_k_step *)step, (float *)partial,
                          out, q_heads, 1, head, seq, split_len,
                          ammon_attention_splits(seq, split_len), 0, seq, 0, nullptr, 0, 0, 0, 0, 0};
   const uint32_t grid = q_heads * cdiv(head, 8);
   if (next_w) {
-    AMMON_CHECK(valid_dtype(next_dtype), "attention_combine: unknown next weight dtype %d",
-                (int)next_dtype);
-    AMMON_CHECK(next_rows > 0 && next_n > 0, "attention_combine: empty next matrix (%u x %u)",
-                next_rows, next_n);
     // The next GEMV (a RESIDUAL-mode ammon_gemv of next_rows x next_n) gives
     // row block j (kGemvRowsPerWave * kGemvWaves rows) to workgroup j % its
     // grid, which runs on XCD (j % grid) % 8, and requests each row's first
@@ -488,7 +490,9 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
     // has a workgroup of its own and both grids are whole multiples of the 8
     // XCDs.  Warming half a tile bought nothing when measured (a wave waits
     // for the slowest of its loads), and more than ~20 MB overflows the 8
-    // XCDs' 4 MB L2s.
+    // XCDs' 4 MB L2s.  A workgroup warms whole blocks (its buffer covers
+    // rows_per_wg rows), so a ragged last block would reach past the matrix:
+    // such a matrix is not warmed.
     const uint64_t row_bytes = (uint64_t)next_n * dsize(next_dtype);
     const uint32_t rows_per_wg = kGemvRowsPerWave * kGemvWaves;
     const uint32_t blocks = cdiv(next_rows, rows_per_wg);
@@ -497,7 +501,8 @@ ammon_status ammon_attention_combine_warm(ammon_runtime *rt, ammon_stream stream
         gemv_grid_for(rt, next_w, next_dtype, next_n, next_rows, &tile_row_bytes);
     const uint64_t want = warm_row_bytes ? warm_row_bytes : tile_row_bytes;
     const uint64_t bytes = std::min<uint64_t>(want, row_bytes) / 128 * 128;
-    if (gemv_grid % 8 == 0 && grid % 8 == 0 && blocks == gemv_grid && blocks <= grid &&
+    if (next_rows % rows_per_wg == 0 && gemv_grid % 8 == 0 && grid % 8 == 0 &&
+        blocks == gemv_grid && blocks <= grid &&
         bytes > 0 && (uint64_t)rows_per_wg * row_bytes < (1ull << 31) &&
         bytes / 128 * rows_per_wg <= (uint64_t)kWorkgroup * 4 &&
         (uint64_t)blocks * rows_per_wg * bytes <= kWarmMaxBytes) {

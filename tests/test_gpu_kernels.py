@@ -340,8 +340,8 @@ def test_combine_warm_matches_combine(rt):
     # (bit for bit) whether it warms the next GEMV's rows (the Llama-3-8B wo,
     # 4096 x 4096 bf16: one row block per workgroup), warms whole rows, or
     # skips warming (a position below the threshold, a matrix whose blocks
-    # do not line up with the merge grid, no matrix); a bad next matrix is a
-    # validation error.
+    # do not line up with the merge grid, one whose last block is ragged, no
+    # matrix); a bad next matrix is a validation error.
     q_heads, kv_heads, head, seq, split = 32, 8, 128, 2048, 128
     qh = oracle.normal(q_heads * head, 181).reshape(q_heads, head)
     kh = oracle.storage(oracle.normal(seq * kv_heads * head, 182), BF16).reshape(
@@ -366,7 +366,8 @@ def test_combine_warm_matches_combine(rt):
         want = down(plain, (q_heads, head))
         assert rel_err(want, oracle.attention(qh, kh, vh, BF16, pos)) <= RTOL, pos
         for nxt, rows, n, row_bytes in ((wo, dim, dim, 0), (wo, dim, dim, 2 * dim),
-                                        (wo, 100, dim, 0), (None, 0, 0, 0)):
+                                        (wo, 100, dim, 0), (wo, dim - 4, dim, 0),
+                                        (None, 0, 0, 0)):
             rt.fill(warm, F32, q_heads * head, float("nan"))
             call("ammon_attention_combine_warm", rt.handle, None, part, q_heads, head, seq, step,
                  split, warm, nxt, BF16, rows, n, row_bytes, 1024)
